@@ -1,0 +1,358 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X flash-attention forward (one GPU).
+
+Headline (``value``): GQA prefill, non-causal, B=1, H_q=32, H_kv=8, D=128,
+Q_len = KV_len = 4096, fp16 in / fp32 out -- BASELINE.json configs[2], the
+"prefill TFLOPS @S=4096" half of the metric.  A step is one forward pass over
+that batch (one kernel launch); inputs are resident in HBM before timing.
+
+Also reported in the same JSON line (the "decode latency + HBM GB/s @KV=4096"
+half of the metric):
+  * ``decode``    -- configs[1]: B=1, H_q=32, H_kv=8, D=128, Q_len=1,
+                     KV=4096.  Its 16.8 MB working set fits the 256 MB
+                     Infinity Cache, so each step reads the next of
+                     ``--decode-sets`` distinct Q/K/V sets (> 512 MB total) and
+                     the figure is an HBM figure, not a cache figure.
+  * ``decode_b32`` -- configs[4]: B=32, KV=8192 (1.07 GB of unique K/V per
+                     step), the clean HBM-streaming case.
+  * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep)
+                     and the MQA D=64 configs[3].
+
+FLOPs = 4*B*H_q*q_len*kv_len*D and bytes = fp16 Q + unique fp16 K,V + fp32 O
+(tests/bench_flash_attn.cu:125-131).  ``roofline.achieved`` divides those by
+the kernel's average duration measured here with HIP events around each
+launch on the launch stream.  ``cpu_baseline`` times the repo's NumPy
+restatement of the reference's CPU path (kernel_models/flash_attn.py:250-265)
+on a bounded sample of the same workload on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+METRIC = "prefill TFLOPS @S=4096 GQA D=128; decode latency + HBM GB/s @KV=4096"
+PEAK_FP16_TFLOPS = 2516.6   # MI355X dense fp16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+REF_PREFILL_S4096_TFLOPS = 19.3   # reference, RTX 5070 (README.md:49)
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_prefill_s4096.json")
+
+
+def flops(B, H_q, q, kv, D):
+    return 4.0 * B * H_q * q * kv * D
+
+
+def nbytes(B, H_q, H_kv, q, kv, D):
+    qn, kvn = B * H_q * q * D, B * H_kv * kv * D
+    return 2.0 * qn + 4.0 * kvn + 4.0 * qn
+
+
+def _inputs(torch, B, H_q, H_kv, q, kv, D, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    Q = torch.randn((B, H_q, q, D), generator=g, device="cuda", dtype=torch.float32).half()
+    K = torch.randn((B, H_kv, kv, D), generator=g, device="cuda", dtype=torch.float32).half()
+    V = torch.randn((B, H_kv, kv, D), generator=g, device="cuda", dtype=torch.float32).half()
+    return Q, K, V
+
+
+class Runner:
+    """Pre-resolved kf_attn_fwd call (no allocation inside the timed loop)."""
+
+    def __init__(self, torch, kf, sets, D):
+        self.torch, self.kf = torch, kf
+        Q, K, V = sets[0]
+        B, H_q, q, _ = Q.shape
+        _, H_kv, kv, _ = K.shape
+        self.shape = (B, q, kv, H_q, H_kv, D)
+        self.plan = kf.plan(B, q, kv, H_q, H_kv, D)
+        self.ws_bytes = self.plan.workspace_bytes
+        self.ws = torch.empty(max(self.ws_bytes, 256), dtype=torch.uint8, device="cuda")
+        self.sets = sets
+        self.outs = [torch.empty((B, H_q, q, D), dtype=torch.float32, device="cuda") for _ in sets]
+        self.stream = torch.cuda.current_stream()
+        self.lib = kf.load_library()
+        self.i = 0
+
+    def launch(self):
+        j = self.i % len(self.sets)
+        self.i += 1
+        Q, K, V = self.sets[j]
+        B, q, kv, H_q, H_kv, D = self.shape
+        st = self.lib.kf_attn_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), self.outs[j].data_ptr(),
+                                  None, None, B, q, kv, H_q, H_kv, D,
+                                  self.ws.data_ptr() if self.ws_bytes else None, self.ws_bytes,
+                                  self.stream.cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"kf_attn_fwd failed: {self.kf.status_string(st)}")
+        return j
+
+
+def time_steps(torch, runner, steps, warmup):
+    """Whole-step wall time over `steps` back-to-back launches, plus the
+    average per-launch duration from an event pair around every launch."""
+    for _ in range(warmup):
+        runner.launch()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(runner.stream)
+    for _ in range(steps):
+        runner.launch()
+    t1.record(runner.stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / steps
+    # Per-launch durations (separate pass so the event records do not perturb
+    # the back-to-back timing above).
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for a, b in evs:
+        a.record(runner.stream)
+        runner.launch()
+        b.record(runner.stream)
+    torch.cuda.synchronize()
+    per = [a.elapsed_time(b) for a, b in evs]
+    return ms_step, statistics.mean(per), statistics.median(per)
+
+
+def parity_spot_check(torch, runner, heads):
+    """Compare the last outputs on a few heads with the fp64 oracle."""
+    from oracle import attn_oracle as orc
+    import numpy as np
+
+    j = (runner.i - 1) % len(runner.sets)
+    Q, K, V = (t.cpu().numpy() for t in runner.sets[j])
+    O = runner.outs[j].cpu().numpy()
+    H_q, H_kv = Q.shape[1], K.shape[1]
+    worst = (0.0, 0.0)
+    for b, h in heads:
+        hk = h // (H_q // H_kv)
+        ref, _, _ = orc.sdpa(Q[b:b + 1, h:h + 1], K[b:b + 1, hk:hk + 1], V[b:b + 1, hk:hk + 1])
+        ok, mx, rel = orc.within_tolerance(O[b:b + 1, h:h + 1], ref)
+        if not ok:
+            raise AssertionError(f"bench parity failed on head ({b},{h}): max_abs={mx} rel={rel}")
+        worst = (max(worst[0], mx), max(worst[1], rel))
+    return {"heads": [list(x) for x in heads], "max_abs": worst[0], "rel_l2": worst[1],
+            "atol": orc.ATOL, "rtol": orc.RTOL, "ok": True}
+
+
+def cpu_baseline(seconds_target=15.0):
+    """Time the NumPy restatement of the reference's CPU path (fp32 SDPA per
+    head) on a bounded sample of the headline workload: a subset of the 32
+    query heads at S=4096, scaled to TFLOPS."""
+    import numpy as np
+
+    from oracle import attn_oracle as orc
+
+    S, D, H_q, H_kv = 4096, 128, 32, 8
+    q, k, v = orc.normal_fp16_inputs(1, H_q, H_kv, S, S, D, 1)
+    q, k, v = q.astype(np.float32), k.astype(np.float32), v.astype(np.float32)
+    orc.sdpa_fp32_reference_style(q[:, :1], k[:, :1], v[:, :1])   # warm-up, 1 head
+    t = time.perf_counter()
+    orc.sdpa_fp32_reference_style(q[:, :1], k[:, :1], v[:, :1])
+    one = time.perf_counter() - t
+    n_heads = int(max(1, min(H_q, seconds_target / 3.0 / max(one, 1e-3))))
+    runs = []
+    for _ in range(3):
+        t = time.perf_counter()
+        orc.sdpa_fp32_reference_style(q[:, :n_heads], k[:, :(n_heads + 3) // 4],
+                                      v[:, :(n_heads + 3) // 4])
+        runs.append(time.perf_counter() - t)
+    sec = statistics.median(runs)
+    tflops = flops(1, n_heads, S, S, D) / sec / 1e12
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    threads = os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS")
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(tflops, 4), "unit": "TFLOPS",
+        "cores": int(threads) if threads and threads.isdigit() else cores,
+        "kind": "port",
+        "sample": (f"prefill S=4096 GQA D=128, {n_heads} of 32 query heads, fp32 NumPy SDPA "
+                   f"(oracle.sdpa_fp32_reference_style = kernel_models/flash_attn.py:250-265), "
+                   f"median of 3 runs = {sec:.2f} s; cpu '{cpu_model}', "
+                   f"affinity {cores} cores, BLAS threads {threads or 'default'}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--decode-sets", type=int, default=40,
+                    help="distinct Q/K/V sets rotated through for the KV=4096 decode")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "decode", "decode_b32", "copy"], default=None,
+                    help="run one workload only (for rocprof counter passes); prints no JSON")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}); the attention forward shards by KV head with no "
+              "communication, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import kernelfoundry_amd as kf
+
+    if not torch.cuda.is_available():
+        print("bench.py needs the MI355X GPU", file=sys.stderr)
+        sys.exit(1)
+    kf.load_library()
+    steps, warmup = args.steps, args.warmup
+
+    if args.only == "copy":
+        # Plain copy of known size, for calibrating FETCH_SIZE / WRITE_SIZE.
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy: {steps} x {src.numel()} bytes", flush=True)
+        return
+
+    results = {}
+
+    def run_prefill(S, H_kv=8, D=128, steps_=steps, check=None):
+        sets = [_inputs(torch, 1, 32, H_kv, S, S, D, 1234 + S)]
+        r = Runner(torch, kf, sets, D)
+        ms, kern_mean, kern_med = time_steps(torch, r, steps_, warmup)
+        f = flops(1, 32, S, S, D)
+        out = {"S": S, "H_kv": H_kv, "D": D, "ms": ms, "tflops": f / (ms * 1e9),
+               "kernel_ms_mean": kern_mean, "kernel_tflops": f / (kern_mean * 1e9),
+               "grid_blocks": r.plan.grid_blocks}
+        if check:
+            out["parity"] = parity_spot_check(torch, r, check)
+        return out
+
+    if args.only in (None, "prefill"):
+        print("bench: prefill S=4096 GQA D=128", file=sys.stderr, flush=True)
+        results["prefill"] = run_prefill(4096, check=[(0, 0), (0, 31)] if args.only is None else None)
+        if args.only:
+            return
+
+    def run_decode(B, kv, n_sets, D=128, H_kv=8):
+        sets = [_inputs(torch, B, 32, H_kv, 1, kv, D, 99 + i) for i in range(n_sets)]
+        r = Runner(torch, kf, sets, D)
+        ms, kern_mean, kern_med = time_steps(torch, r, steps, warmup)
+        by = nbytes(B, 32, H_kv, 1, kv, D)
+        out = {"B": B, "kv_len": kv, "D": D, "H_kv": H_kv, "sets_rotated": n_sets,
+               "latency_us": ms * 1e3, "gbs": by / (ms * 1e6),
+               "launch_us_mean": kern_mean * 1e3, "launch_gbs": by / (kern_mean * 1e6),
+               "bytes": by, "path": r.plan.path, "splits": r.plan.num_splits}
+        return out, r
+
+    if args.only in (None, "decode"):
+        print("bench: decode B=1 KV=4096", file=sys.stderr, flush=True)
+        results["decode"], rdec = run_decode(1, 4096, args.decode_sets)
+        if args.only:
+            return
+        results["decode"]["parity"] = parity_spot_check(torch, rdec, [(0, 0), (0, 17)])
+        del rdec
+    if args.only in (None, "decode_b32"):
+        print("bench: decode B=32 KV=8192", file=sys.stderr, flush=True)
+        results["decode_b32"], rb = run_decode(32, 8192, 1)
+        if args.only:
+            return
+        results["decode_b32"]["parity"] = parity_spot_check(torch, rb, [(0, 0), (31, 31)])
+        del rb
+
+    print("bench: sweep", file=sys.stderr, flush=True)
+    sweep = [run_prefill(S) for S in (512, 1024, 2048)]
+    sweep.append(run_prefill(2048, H_kv=1, D=64))
+    dq, _ = run_decode(1, 2048, 1, D=64, H_kv=1)
+    sweep.append({"mqa_decode_d64": dq})
+    torch.cuda.empty_cache()
+
+    pre = results["prefill"]
+    dec = results["decode"]
+    b32 = results["decode_b32"]
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(pre["tflops"], 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(pre["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(pre["tflops"] / REF_PREFILL_S4096_TFLOPS, 2),
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "GQA prefill non-causal, fp16 Q/K/V N(0,1), fp32 O",
+                   "B": 1, "H_q": 32, "H_kv": 8, "D": 128, "q_len": 4096, "kv_len": 4096,
+                   "baseline_config": "configs[2]"},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "kf_attn_prefill_kernel<128>",
+            "achieved": round(pre["kernel_tflops"], 2),
+            "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(pre["kernel_tflops"] / PEAK_FP16_TFLOPS, 4),
+            "traffic": traffic,
+            "algorithmic_flops_per_launch": flops(1, 32, 4096, 4096, 128),
+            "kernel_ms_mean": round(pre["kernel_ms_mean"], 5),
+        },
+        "decode": {
+            "config": "configs[1]: B=1 H_q=32 H_kv=8 D=128 q_len=1 kv_len=4096",
+            "latency_us": round(dec["latency_us"], 3),
+            "hbm_gbs": round(dec["gbs"], 1),
+            "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(dec["gbs"] / PEAK_HBM_GBS, 4),
+                         "bytes_per_launch": dec["bytes"]},
+            "path": dec["path"], "splits": dec["splits"],
+            "sets_rotated": dec["sets_rotated"],
+            "launch_us_mean": round(dec["launch_us_mean"], 3),
+            "parity": dec["parity"],
+        },
+        "decode_b32": {
+            "config": "configs[4]: B=32 H_q=32 H_kv=8 D=128 q_len=1 kv_len=8192",
+            "latency_us": round(b32["latency_us"], 2),
+            "hbm_gbs": round(b32["gbs"], 1),
+            "roofline": {"bound": "hbm", "achieved": round(b32["gbs"], 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(b32["gbs"] / PEAK_HBM_GBS, 4),
+                         "bytes_per_launch": b32["bytes"]},
+            "path": b32["path"], "splits": b32["splits"],
+            "parity": b32["parity"],
+        },
+        "sweep": sweep,
+        "parity": pre.get("parity"),
+    }
+    if not args.no_cpu_baseline:
+        print("bench: cpu baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,122 @@
+/*
+ * kf/attn.h -- C ABI of the MI355X (gfx950) flash-attention forward.
+ *
+ * This is the drop-in boundary for the reference's attention launchers:
+ *   - launch_flash_attn      tests/test_flash_attn.cu:52-113  (synchronous,
+ *                            q_len == kv_len == S, launcher-owned scratch)
+ *   - launch_once            tests/bench_flash_attn.cu:39-54  (asynchronous,
+ *                            separate q_len / kv_len, caller-owned Mi / Li)
+ *   - flash_attn_kernel<D>   kernels/flash_attn.cu:384-398    (the device
+ *                            entry those launchers wrap; not exported here)
+ *
+ * Plain C types only: device pointers, sizes and an opaque stream handle
+ * (a hipStream_t passed as void*; NULL is the default stream).  No C++
+ * exceptions cross this boundary; every entry point returns a status code.
+ *
+ * Tensor layout contract (identical to the reference's, flash_attn.cu:364-370):
+ *   Q  [B, H_q,  q_len,  D]  fp16 bits (uint16_t), contiguous row-major
+ *   K  [B, H_kv, kv_len, D]  fp16 bits
+ *   V  [B, H_kv, kv_len, D]  fp16 bits
+ *   O  [B, H_q,  q_len,  D]  fp32
+ *   Mi [B, H_q,  q_len]      fp32, optional: max_j s_ij over the scaled scores
+ *                            s = q.k / sqrt(D)
+ *   Li [B, H_q,  q_len]      fp32, optional: sum_j exp(s_ij - Mi)
+ * Query head h_q reads KV head h_q / (H_q / H_kv) (flash_attn.cu:406); H_q
+ * must be a multiple of H_kv (the reference silently mis-groups otherwise).
+ * Attention is non-causal and the softmax scale is 1/sqrt(D), as in the
+ * reference.  D must be one of the reference's instantiations
+ * {16, 64, 128, 256} (flash_attn.cu:587-600).  All device pointers must be
+ * 16-byte aligned.
+ */
+#ifndef KF_ATTN_H
+#define KF_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes returned by the kf_* entry points. */
+enum kf_status {
+    KF_OK = 0,
+    KF_ERR_HEAD_DIM = 1,   /* D is not 16, 64, 128 or 256                      */
+    KF_ERR_GQA = 2,        /* H_q is not a positive multiple of H_kv            */
+    KF_ERR_SIZE = 3,       /* a size is <= 0 or overflows the kernels' indexing */
+    KF_ERR_NULL = 4,       /* a required pointer is NULL                        */
+    KF_ERR_WORKSPACE = 5,  /* workspace missing or smaller than required        */
+    KF_ERR_ALIGN = 6,      /* a device pointer is not 16-byte aligned           */
+    KF_ERR_HIP = 7         /* a HIP runtime call failed: kf_last_hip_error()    */
+};
+
+/* Which kernels kf_attn_fwd runs for a shape (see kf_attn_plan). */
+enum kf_path {
+    KF_PATH_PREFILL = 0,   /* MFMA prefill kernel, one pass over KV             */
+    KF_PATH_DECODE = 1,    /* split-KV decode kernel, writes final O directly   */
+    KF_PATH_DECODE_SPLIT = 2 /* split-KV decode kernel; the last workgroup of
+                                each KV head merges the partials (one launch) */
+};
+
+typedef struct kf_attn_plan_t {
+    int path;              /* enum kf_path                                      */
+    int rows_per_group;    /* H_q / H_kv * q_len query rows per KV head         */
+    int num_splits;        /* KV partitions per (b, h_kv); 1 = unsplit          */
+    int kv_per_split;      /* KV rows per partition                             */
+    int grid_blocks;       /* workgroups of the main kernel                     */
+    int block_threads;     /* threads per workgroup of the main kernel          */
+    size_t workspace_bytes;/* bytes kf_attn_fwd needs in `workspace`            */
+} kf_attn_plan_t;
+
+/* Describe the dispatch kf_attn_fwd would use.  Validates like kf_attn_fwd
+ * (sizes only, no pointers) and touches no GPU state. */
+int kf_attn_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
+                 kf_attn_plan_t* plan);
+
+/* Bytes of device workspace kf_attn_fwd needs for this shape (0 when the
+ * shape runs without split-KV partials).  Returns 0 for invalid shapes too;
+ * kf_attn_plan reports why. */
+size_t kf_attn_workspace_bytes(int B, int q_len, int kv_len, int H_q, int H_kv, int D);
+
+/* Attention forward, asynchronous on `stream`.
+ *
+ * Replaces launch_once (tests/bench_flash_attn.cu:39-54) and the kernel
+ * launch inside launch_flash_attn (tests/test_flash_attn.cu:92-93):
+ * separate q_len / kv_len (q_len = 1 is decode), optional Mi / Li outputs
+ * (row_max / row_sumexp may be NULL), caller-owned workspace of at least
+ * kf_attn_workspace_bytes() bytes (may be NULL when that is 0; 256-byte
+ * aligned).  The workspace needs no initialisation; it must not be shared by
+ * calls that can run concurrently (e.g. on two streams).
+ * Validation happens before any HIP call; an invalid argument returns its
+ * status code and launches nothing.  Unlike launch_once, which silently
+ * does nothing for an unsupported D (bench_flash_attn.cu:48-52), this
+ * returns KF_ERR_HEAD_DIM. */
+int kf_attn_fwd(const void* Q, const void* K, const void* V, float* O,
+                float* row_max, float* row_sumexp,
+                int B, int q_len, int kv_len, int H_q, int H_kv, int D,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* The reference launcher's contract (tests/test_flash_attn.cu:52-113):
+ * q_len = kv_len = S, scratch allocated and freed by the call, stream
+ * synchronised before returning.  Returns a hipError_t value:
+ * hipSuccess (0), hipErrorInvalidValue for an unsupported D or an invalid
+ * shape, or the HIP error of a failed allocation / launch / sync. */
+int kf_launch_flash_attn(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                         float* O, int B, int S, int H_q, int H_kv, int D,
+                         void* stream);
+
+/* Human-readable text for a kf_status value (static storage). */
+const char* kf_status_string(int status);
+
+/* hipError_t of the last failed HIP call made by a kf_* entry point on the
+ * calling thread (0 if none). */
+int kf_last_hip_error(void);
+
+/* Library version string. */
+const char* kf_version(void);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* KF_ATTN_H */

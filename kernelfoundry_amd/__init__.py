@@ -1,0 +1,194 @@
+"""kernelfoundry_amd -- MI355X (gfx950) flash-attention forward.
+
+Python host side over the C ABI of ``lib/libkf_attn.so`` (include/kf/attn.h).
+The compute runs only in the HIP kernels of that library; there is no CPU or
+PyTorch fallback: if the library is missing, every entry point raises.
+
+Interface, mirroring the reference harness (sviraaj/kernelfoundry):
+
+* ``launch_flash_attn(Q, K, V, O, B, S, H_q, H_kv, D, stream=0)`` -- the
+  reference launcher (tests/test_flash_attn.cu:52-113) on raw device
+  pointers: q_len = kv_len = S, synchronous, returns a hipError_t value
+  (0 on success, hipErrorInvalidValue = 1 for an unsupported D or shape).
+* ``attn_fwd(Q, K, V, ...)`` -- asynchronous forward on torch device tensors
+  (torch provides device memory and the stream; it is plumbing only), with
+  separate q_len / kv_len (decode) and optional Mi / Li outputs, as the
+  bench's ``launch_once`` (tests/bench_flash_attn.cu:39-54).
+* ``attn_fwd_ptr(...)`` -- the same on raw pointers, returning the kf status.
+* ``plan(B, q_len, kv_len, H_q, H_kv, D)`` -- which kernels run, GPU-free.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from dataclasses import dataclass
+
+__all__ = [
+    "KfError", "LIB_PATH", "load_library", "plan", "workspace_bytes", "attn_fwd",
+    "attn_fwd_ptr", "launch_flash_attn", "status_string", "exported_symbols",
+    "KF_OK", "KF_ERR_HEAD_DIM", "KF_ERR_GQA", "KF_ERR_SIZE", "KF_ERR_NULL",
+    "KF_ERR_WORKSPACE", "KF_ERR_ALIGN", "KF_ERR_HIP", "PATH_NAMES",
+]
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "lib", "libkf_attn.so")
+HEADER_PATH = os.path.join(os.path.dirname(_PKG), "include", "kf", "attn.h")
+
+KF_OK = 0
+KF_ERR_HEAD_DIM = 1
+KF_ERR_GQA = 2
+KF_ERR_SIZE = 3
+KF_ERR_NULL = 4
+KF_ERR_WORKSPACE = 5
+KF_ERR_ALIGN = 6
+KF_ERR_HIP = 7
+
+PATH_NAMES = {0: "prefill", 1: "decode", 2: "decode_split"}
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+
+
+class KfError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"kf status {status}: {message}")
+        self.status = status
+
+
+class _PlanStruct(ctypes.Structure):
+    _fields_ = [
+        ("path", ctypes.c_int),
+        ("rows_per_group", ctypes.c_int),
+        ("num_splits", ctypes.c_int),
+        ("kv_per_split", ctypes.c_int),
+        ("grid_blocks", ctypes.c_int),
+        ("block_threads", ctypes.c_int),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+@dataclass(frozen=True)
+class Plan:
+    path: str
+    rows_per_group: int
+    num_splits: int
+    kv_per_split: int
+    grid_blocks: int
+    block_threads: int
+    workspace_bytes: int
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load libkf_attn.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: build it with `python -m kernelfoundry_amd.build` "
+            "(or __graft_entry__.build()); there is no fallback implementation")
+    lib = ctypes.CDLL(path)
+    i, p, sz = ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+    lib.kf_attn_plan.argtypes = [i] * 6 + [ctypes.POINTER(_PlanStruct)]
+    lib.kf_attn_plan.restype = i
+    lib.kf_attn_workspace_bytes.argtypes = [i] * 6
+    lib.kf_attn_workspace_bytes.restype = sz
+    lib.kf_attn_fwd.argtypes = [p, p, p, p, p, p] + [i] * 6 + [p, sz, p]
+    lib.kf_attn_fwd.restype = i
+    lib.kf_launch_flash_attn.argtypes = [p, p, p, p] + [i] * 5 + [p]
+    lib.kf_launch_flash_attn.restype = i
+    lib.kf_status_string.argtypes = [i]
+    lib.kf_status_string.restype = ctypes.c_char_p
+    lib.kf_last_hip_error.argtypes = []
+    lib.kf_last_hip_error.restype = i
+    lib.kf_version.argtypes = []
+    lib.kf_version.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def exported_symbols(header: str = HEADER_PATH):
+    """Names of the functions declared in include/kf/attn.h."""
+    text = open(header).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(kf_\w+)\s*\(", text, re.M)))
+
+
+def status_string(status: int) -> str:
+    return load_library().kf_status_string(int(status)).decode()
+
+
+def plan(B, q_len, kv_len, H_q, H_kv, D) -> Plan:
+    out = _PlanStruct()
+    st = load_library().kf_attn_plan(B, q_len, kv_len, H_q, H_kv, D, ctypes.byref(out))
+    if st != KF_OK:
+        raise KfError(st, status_string(st))
+    return Plan(PATH_NAMES[out.path], out.rows_per_group, out.num_splits, out.kv_per_split,
+                out.grid_blocks, out.block_threads, int(out.workspace_bytes))
+
+
+def workspace_bytes(B, q_len, kv_len, H_q, H_kv, D) -> int:
+    return int(load_library().kf_attn_workspace_bytes(B, q_len, kv_len, H_q, H_kv, D))
+
+
+def attn_fwd_ptr(Q, K, V, O, Mi, Li, B, q_len, kv_len, H_q, H_kv, D, workspace=0,
+                 workspace_bytes=0, stream=0) -> int:
+    """kf_attn_fwd on raw device addresses (ints); returns the kf status."""
+    return int(load_library().kf_attn_fwd(Q, K, V, O, Mi or None, Li or None, B, q_len, kv_len,
+                                          H_q, H_kv, D, workspace or None, workspace_bytes,
+                                          stream or None))
+
+
+def launch_flash_attn(Q, K, V, O, B, S, H_q, H_kv, D, stream=0) -> int:
+    """Reference launcher contract on raw device addresses; returns hipError_t."""
+    return int(load_library().kf_launch_flash_attn(Q, K, V, O, B, S, H_q, H_kv, D, stream or None))
+
+
+def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=None):
+    """Attention forward on torch tensors resident on the GPU.
+
+    Q [B, H_q, q_len, D] fp16, K/V [B, H_kv, kv_len, D] fp16, contiguous.
+    Returns O [B, H_q, q_len, D] fp32, or (O, Mi, Li) with ``return_stats``.
+    Asynchronous on ``stream`` (default: torch's current stream).
+    """
+    import torch
+
+    if Q.dtype != torch.float16 or K.dtype != torch.float16 or V.dtype != torch.float16:
+        raise TypeError("Q, K, V must be float16")
+    if not (Q.is_cuda and K.is_cuda and V.is_cuda):
+        raise ValueError("Q, K, V must be GPU tensors")
+    if not (Q.is_contiguous() and K.is_contiguous() and V.is_contiguous()):
+        raise ValueError("Q, K, V must be contiguous [B, H, S, D]")
+    if Q.dim() != 4 or K.dim() != 4 or K.shape != V.shape:
+        raise ValueError("expected Q [B,H_q,q_len,D] and K, V [B,H_kv,kv_len,D]")
+    B, H_q, q_len, D = Q.shape
+    Bk, H_kv, kv_len, Dk = K.shape
+    if Bk != B or Dk != D:
+        raise ValueError("Q and K/V disagree on B or D")
+    if out is None:
+        out = torch.empty((B, H_q, q_len, D), dtype=torch.float32, device=Q.device)
+    Mi = Li = None
+    if return_stats:
+        Mi = torch.empty((B, H_q, q_len), dtype=torch.float32, device=Q.device)
+        Li = torch.empty_like(Mi)
+    need = workspace_bytes(B, q_len, kv_len, H_q, H_kv, D)
+    if stream is None:
+        stream = torch.cuda.current_stream(Q.device)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=Q.device)
+        workspace.record_stream(stream)
+    st = attn_fwd_ptr(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(),
+                      Mi.data_ptr() if Mi is not None else 0,
+                      Li.data_ptr() if Li is not None else 0,
+                      B, q_len, kv_len, H_q, H_kv, D,
+                      workspace.data_ptr() if (need and workspace is not None) else 0,
+                      need, stream.cuda_stream)
+    if st != KF_OK:
+        msg = status_string(st)
+        if st == KF_ERR_HIP:
+            msg += f" (hipError_t {load_library().kf_last_hip_error()})"
+        raise KfError(st, msg)
+    return (out, Mi, Li) if return_stats else out

@@ -1,0 +1,240 @@
+// attn_capi.hip -- C ABI of libkf_attn.so: validation, dispatch plan, launches.
+//
+// Entry points are declared in include/kf/attn.h.  Every argument check runs
+// before the first HIP call, so invalid calls are rejected on any host (the
+// CPU-only tests rely on that) and never reach a kernel.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <climits>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+
+#include "attn_kernels.h"
+#include "kf/attn.h"
+
+namespace {
+
+constexpr int kNumCUs = 256;            // MI355X compute units
+constexpr int kDecodeMaxRows = 32;      // query rows per KV head on the decode path
+constexpr int kDecodeTargetBlocks = 2 * kNumCUs;
+constexpr int kDecodeMinSplitRows = 4 * kf::kDecodeStage;  // one stage per wave
+constexpr size_t kWsAlign = 256;
+
+thread_local int g_last_hip_error = 0;
+std::atomic<unsigned> g_epoch{0};  // split-merge ticket epochs, unique per call
+
+unsigned next_epoch() {
+    unsigned e = g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
+    if (e == 0u) e = g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
+    return e;
+}
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+bool supported_head_dim(int D) { return D == 16 || D == 64 || D == 128 || D == 256; }
+
+struct Plan {
+    int path;
+    int R;
+    int n_groups;
+    int rows_total;
+    int n_splits;
+    int kv_per_split;
+    int grid;
+    int threads;
+    size_t ws_bytes;
+    size_t ws_o_off, ws_m_off, ws_l_off, ws_t_off;
+};
+
+int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) {
+    if (B <= 0 || q_len <= 0 || kv_len <= 0 || H_q <= 0 || H_kv <= 0) return KF_ERR_SIZE;
+    if (!supported_head_dim(D)) return KF_ERR_HEAD_DIM;
+    if (H_q % H_kv != 0) return KF_ERR_GQA;
+    const long long ratio = H_q / H_kv;
+    const long long R = ratio * q_len;
+    const long long n_groups = (long long)B * H_kv;
+    const long long rows_total = n_groups * R;
+    // In-head offsets are 32-bit (row * D, kv * D); group bases are 64-bit.
+    if (R * D > INT_MAX || (long long)kv_len * D > INT_MAX || rows_total > INT_MAX)
+        return KF_ERR_SIZE;
+
+    Plan p{};
+    p.R = (int)R;
+    p.n_groups = (int)n_groups;
+    p.rows_total = (int)rows_total;
+    if (R <= kDecodeMaxRows) {
+        long long splits = (kDecodeTargetBlocks + n_groups - 1) / n_groups;
+        const long long max_splits = (kv_len + kDecodeMinSplitRows - 1) / kDecodeMinSplitRows;
+        if (splits > max_splits) splits = max_splits;
+        if (splits < 1) splits = 1;
+        long long per = (kv_len + splits - 1) / splits;
+        per = (per + kf::kDecodeStage - 1) / kf::kDecodeStage * kf::kDecodeStage;
+        splits = (kv_len + per - 1) / per;
+        if (n_groups * splits > INT_MAX) return KF_ERR_SIZE;
+        p.n_splits = (int)splits;
+        p.kv_per_split = (int)per;
+        p.grid = (int)(n_groups * splits);
+        p.threads = kf::kDecodeThreads;
+        p.path = splits > 1 ? KF_PATH_DECODE_SPLIT : KF_PATH_DECODE;
+    } else {
+        const long long row_tiles = (R + kf::kPrefillRows - 1) / kf::kPrefillRows;
+        if (n_groups * row_tiles > INT_MAX) return KF_ERR_SIZE;
+        p.n_splits = 1;
+        p.kv_per_split = kv_len;
+        p.grid = (int)(n_groups * row_tiles);
+        p.threads = kf::kPrefillThreads;
+        p.path = KF_PATH_PREFILL;
+    }
+    if (p.path == KF_PATH_DECODE_SPLIT) {
+        const size_t parts = (size_t)p.n_splits * (size_t)rows_total;
+        p.ws_o_off = 0;
+        p.ws_m_off = align_up(parts * D * sizeof(float), kWsAlign);
+        p.ws_l_off = p.ws_m_off + align_up(parts * sizeof(float), kWsAlign);
+        p.ws_t_off = p.ws_l_off + align_up(parts * sizeof(float), kWsAlign);
+        p.ws_bytes = p.ws_t_off + align_up((size_t)n_groups * sizeof(unsigned long long), kWsAlign);
+    }
+    *pl = p;
+    return KF_OK;
+}
+
+inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+int hip_fail(hipError_t e) {
+    g_last_hip_error = (int)e;
+    return KF_ERR_HIP;
+}
+
+template <int D>
+hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t stream) {
+    if (pl.path == KF_PATH_PREFILL) {
+        kf::kf_attn_prefill_kernel<D><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+        return hipGetLastError();
+    }
+    kf::kf_attn_decode_kernel<D><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+int kf_attn_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, kf_attn_plan_t* plan) {
+    if (!plan) return KF_ERR_NULL;
+    Plan pl;
+    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, &pl);
+    if (st != KF_OK) return st;
+    plan->path = pl.path;
+    plan->rows_per_group = pl.R;
+    plan->num_splits = pl.n_splits;
+    plan->kv_per_split = pl.kv_per_split;
+    plan->grid_blocks = pl.grid;
+    plan->block_threads = pl.threads;
+    plan->workspace_bytes = pl.ws_bytes;
+    return KF_OK;
+}
+
+size_t kf_attn_workspace_bytes(int B, int q_len, int kv_len, int H_q, int H_kv, int D) {
+    Plan pl;
+    if (make_plan(B, q_len, kv_len, H_q, H_kv, D, &pl) != KF_OK) return 0;
+    return pl.ws_bytes;
+}
+
+int kf_attn_fwd(const void* Q, const void* K, const void* V, float* O, float* row_max,
+                float* row_sumexp, int B, int q_len, int kv_len, int H_q, int H_kv, int D,
+                void* workspace, size_t workspace_bytes, void* stream) {
+    Plan pl;
+    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, &pl);
+    if (st != KF_OK) return st;
+    if (!Q || !K || !V || !O) return KF_ERR_NULL;
+    if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O)) return KF_ERR_ALIGN;
+    if (pl.ws_bytes > 0) {
+        if (!workspace || workspace_bytes < pl.ws_bytes) return KF_ERR_WORKSPACE;
+        if ((reinterpret_cast<uintptr_t>(workspace) & (kWsAlign - 1)) != 0) return KF_ERR_ALIGN;
+    }
+
+    kf::AttnParams prm{};
+    prm.Q = static_cast<const uint16_t*>(Q);
+    prm.K = static_cast<const uint16_t*>(K);
+    prm.V = static_cast<const uint16_t*>(V);
+    prm.O = O;
+    prm.Mi = row_max;
+    prm.Li = row_sumexp;
+    if (pl.ws_bytes > 0) {
+        char* ws = static_cast<char*>(workspace);
+        prm.Opart = reinterpret_cast<float*>(ws + pl.ws_o_off);
+        prm.Mpart = reinterpret_cast<float*>(ws + pl.ws_m_off);
+        prm.Lpart = reinterpret_cast<float*>(ws + pl.ws_l_off);
+        prm.tickets = reinterpret_cast<unsigned long long*>(ws + pl.ws_t_off);
+        prm.epoch = next_epoch();
+    }
+    prm.rows_per_group = pl.R;
+    prm.kv_len = kv_len;
+    prm.row_tiles = (pl.R + kf::kPrefillRows - 1) / kf::kPrefillRows;
+    prm.n_splits = pl.n_splits;
+    prm.kv_per_split = pl.kv_per_split;
+    prm.rows_total = pl.rows_total;
+    const double scale = 1.0 / __builtin_sqrt((double)D);
+    prm.scale = 1.0f / __builtin_sqrtf((float)D);  // the reference's fp32 scale
+    prm.scale_log2 = (float)(scale * 1.4426950408889634);
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    switch (D) {
+        case 16: e = launch_all<16>(pl, prm, s); break;
+        case 64: e = launch_all<64>(pl, prm, s); break;
+        case 128: e = launch_all<128>(pl, prm, s); break;
+        default: e = launch_all<256>(pl, prm, s); break;
+    }
+    if (e != hipSuccess) return hip_fail(e);
+    return KF_OK;
+}
+
+int kf_launch_flash_attn(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,
+                         int B, int S, int H_q, int H_kv, int D, void* stream) {
+    Plan pl;
+    if (make_plan(B, S, S, H_q, H_kv, D, &pl) != KF_OK) return (int)hipErrorInvalidValue;
+    if (!Q || !K || !V || !O || !aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
+        return (int)hipErrorInvalidValue;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    void* ws = nullptr;
+    hipError_t e = hipSuccess;
+    if (pl.ws_bytes > 0) {
+        e = hipMalloc(&ws, pl.ws_bytes);
+        if (e != hipSuccess) {
+            g_last_hip_error = (int)e;
+            return (int)e;
+        }
+    }
+    const int st = kf_attn_fwd(Q, K, V, O, nullptr, nullptr, B, S, S, H_q, H_kv, D, ws,
+                               pl.ws_bytes, stream);
+    if (st == KF_ERR_HIP)
+        e = (hipError_t)g_last_hip_error;
+    else if (st != KF_OK)
+        e = hipErrorInvalidValue;
+    if (e == hipSuccess) e = hipStreamSynchronize(s);  // scratch must outlive the kernels
+    if (ws) (void)hipFree(ws);
+    if (e != hipSuccess) g_last_hip_error = (int)e;
+    return (int)e;
+}
+
+const char* kf_status_string(int status) {
+    switch (status) {
+        case KF_OK: return "ok";
+        case KF_ERR_HEAD_DIM: return "unsupported head dimension (D must be 16, 64, 128 or 256)";
+        case KF_ERR_GQA: return "H_q must be a positive multiple of H_kv";
+        case KF_ERR_SIZE: return "invalid size (non-positive or beyond 32-bit in-head indexing)";
+        case KF_ERR_NULL: return "required pointer is NULL";
+        case KF_ERR_WORKSPACE: return "workspace missing or smaller than kf_attn_workspace_bytes()";
+        case KF_ERR_ALIGN: return "device pointer not 16-byte aligned (workspace: 256-byte)";
+        case KF_ERR_HIP: return "HIP runtime error (see kf_last_hip_error)";
+        default: return "unknown status";
+    }
+}
+
+int kf_last_hip_error(void) { return g_last_hip_error; }
+
+const char* kf_version(void) { return "kernelfoundry_amd 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,183 @@
+// test_flash_attn.cpp -- end-to-end correctness of libkf_attn.so from C++.
+//
+// Mirrors the reference harness tests/test_flash_attn.cu: the same 18 prefill
+// cases (:295-318) with the same inputs (std::mt19937 + uniform_real_distribution
+// on [-1, 1], seeds s, s+1, s+2; tests/test_utils.h:27-31), launched through
+// the same launcher signature launch_flash_attn(Q, K, V, O, B, S, H_q, H_kv, D)
+// (:52-59), checked two ways:
+//   * the reference's own bar: max-abs <= 5e-2 against fp32 attention on the
+//     unrounded inputs (:22, :245, :271), and
+//   * this library's bar: max-abs <= 2e-3 and rel-L2 <= 1e-2 against fp64
+//     attention on the fp16-rounded inputs the GPU actually saw.
+// It adds what the reference never tests: Q_len = 1 decode (GQA, MQA, batched,
+// split-KV) through the asynchronous launcher, and the Mi / Li outputs.
+// The CPU references come from oracle/cpu_attn.c (test infrastructure).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <random>
+#include <vector>
+
+#include "kf/flash_attn.hpp"
+
+extern "C" {
+int kf_oracle_attn_f32(const float*, const float*, const float*, float*, float*, float*, int, int,
+                       int, int, int, int);
+int kf_oracle_attn_f64(const double*, const double*, const double*, double*, double*, double*,
+                       int, int, int, int, int, int);
+unsigned short kf_oracle_float_to_half(float);
+float kf_oracle_half_to_float(unsigned short);
+}
+
+#define HIP_CHECK(expr)                                                                  \
+    do {                                                                                 \
+        hipError_t e_ = (expr);                                                          \
+        if (e_ != hipSuccess) {                                                          \
+            std::fprintf(stderr, "HIP error at %s:%d: %s\n", __FILE__, __LINE__,         \
+                         hipGetErrorString(e_));                                         \
+            std::exit(EXIT_FAILURE);                                                     \
+        }                                                                                \
+    } while (0)
+
+static constexpr float kRefTol = 5e-2f;  // the reference's tolerance (test:22)
+static constexpr double kAtol = 2e-3;    // max-abs error bound
+static constexpr double kRtol = 1e-2;    // relative L2 error bound
+
+static void fill_uniform(std::vector<float>& v, float lo, float hi, uint32_t seed) {
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<float> dist(lo, hi);
+    for (float& x : v) x = dist(rng);
+}
+
+struct Errs {
+    double max_abs = 0, rel = 0;
+};
+
+template <typename T>
+static Errs errors(const std::vector<T>& ref, const std::vector<float>& got) {
+    double num = 0, den = 0, mx = 0;
+    for (size_t i = 0; i < ref.size(); ++i) {
+        const double d = (double)got[i] - (double)ref[i];
+        if (!(std::fabs(d) <= mx)) mx = std::fabs(d);  // NaN propagates to mx
+        num += d * d;
+        den += (double)ref[i] * (double)ref[i];
+    }
+    return {mx, den > 0 ? std::sqrt(num / den) : std::sqrt(num)};
+}
+
+static bool run_case(int B, int q_len, int kv_len, int H_q, int H_kv, int D, uint32_t seed,
+                     bool sync_launcher) {
+    std::printf("  B=%d q_len=%d kv_len=%d H_q=%d H_kv=%d D=%d seed=%u ... ", B, q_len, kv_len,
+                H_q, H_kv, D, seed);
+    std::fflush(stdout);
+    const size_t qn = (size_t)B * H_q * q_len * D, kvn = (size_t)B * H_kv * kv_len * D;
+    const size_t rn = (size_t)B * H_q * q_len;
+    std::vector<float> q(qn), k(kvn), v(kvn);
+    fill_uniform(q, -1.f, 1.f, seed);
+    fill_uniform(k, -1.f, 1.f, seed + 1);
+    fill_uniform(v, -1.f, 1.f, seed + 2);
+
+    std::vector<uint16_t> q16(qn), k16(kvn), v16(kvn);
+    std::vector<double> qd(qn), kd(kvn), vd(kvn);
+    for (size_t i = 0; i < qn; ++i) {
+        q16[i] = kf_oracle_float_to_half(q[i]);
+        qd[i] = kf_oracle_half_to_float(q16[i]);
+    }
+    for (size_t i = 0; i < kvn; ++i) {
+        k16[i] = kf_oracle_float_to_half(k[i]);
+        kd[i] = kf_oracle_half_to_float(k16[i]);
+        v16[i] = kf_oracle_float_to_half(v[i]);
+        vd[i] = kf_oracle_half_to_float(v16[i]);
+    }
+    std::vector<float> ref32(qn), m32(rn), l32(rn);
+    std::vector<double> ref64(qn), m64(rn), l64(rn);
+    kf_oracle_attn_f32(q.data(), k.data(), v.data(), ref32.data(), m32.data(), l32.data(), B,
+                       q_len, kv_len, H_q, H_kv, D);
+    kf_oracle_attn_f64(qd.data(), kd.data(), vd.data(), ref64.data(), m64.data(), l64.data(), B,
+                       q_len, kv_len, H_q, H_kv, D);
+
+    uint16_t *dq, *dk, *dv;
+    float *dO, *dM = nullptr, *dL = nullptr;
+    HIP_CHECK(hipMalloc(&dq, qn * 2));
+    HIP_CHECK(hipMalloc(&dk, kvn * 2));
+    HIP_CHECK(hipMalloc(&dv, kvn * 2));
+    HIP_CHECK(hipMalloc(&dO, qn * 4));
+    HIP_CHECK(hipMemcpy(dq, q16.data(), qn * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dk, k16.data(), kvn * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dv, v16.data(), kvn * 2, hipMemcpyHostToDevice));
+    if (sync_launcher) {
+        HIP_CHECK(launch_flash_attn(dq, dk, dv, dO, B, q_len, H_q, H_kv, D));
+    } else {
+        HIP_CHECK(hipMalloc(&dM, rn * 4));
+        HIP_CHECK(hipMalloc(&dL, rn * 4));
+        HIP_CHECK(launch_flash_attn(dq, dk, dv, dO, B, q_len, kv_len, H_q, H_kv, D, nullptr, dM, dL));
+    }
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<float> got(qn), gm(rn), gl(rn);
+    HIP_CHECK(hipMemcpy(got.data(), dO, qn * 4, hipMemcpyDeviceToHost));
+    if (!sync_launcher) {
+        HIP_CHECK(hipMemcpy(gm.data(), dM, rn * 4, hipMemcpyDeviceToHost));
+        HIP_CHECK(hipMemcpy(gl.data(), dL, rn * 4, hipMemcpyDeviceToHost));
+        (void)hipFree(dM);
+        (void)hipFree(dL);
+    }
+    (void)hipFree(dq);
+    (void)hipFree(dk);
+    (void)hipFree(dv);
+    (void)hipFree(dO);
+
+    const Errs e_ref = errors(ref32, got);
+    const Errs e64 = errors(ref64, got);
+    bool ok = e_ref.max_abs <= kRefTol && e64.max_abs <= kAtol && e64.rel <= kRtol;
+    Errs em{}, el{};
+    if (!sync_launcher) {
+        em = errors(m64, gm);
+        el = errors(l64, gl);
+        ok = ok && em.max_abs <= 1e-4 && el.rel <= 1e-3;
+    }
+    std::printf("%s (ref-bar max_abs=%.3g; fp16-input max_abs=%.3g rel=%.3g", ok ? "PASS" : "FAIL",
+                e_ref.max_abs, e64.max_abs, e64.rel);
+    if (!sync_launcher) std::printf("; Mi max_abs=%.3g Li rel=%.3g", em.max_abs, el.rel);
+    std::printf(")\n");
+    return ok;
+}
+
+int main() {
+    std::printf("=== kernelfoundry_amd flash-attention end-to-end tests (gfx950) ===\n");
+    int failed = 0;
+    struct C { int B, S, H_q, H_kv, D; uint32_t seed; };
+    // The reference's 18 prefill cases (tests/test_flash_attn.cu:295-318).
+    const C ref_cases[] = {
+        {1, 16, 1, 1, 16, 100},   {1, 16, 1, 1, 64, 101},   {1, 64, 1, 1, 128, 102},
+        {1, 17, 1, 1, 128, 103},  {1, 129, 1, 1, 128, 202}, {1, 255, 1, 1, 128, 203},
+        {1, 256, 1, 1, 64, 200},  {1, 256, 1, 1, 128, 201}, {1, 64, 4, 2, 64, 300},
+        {1, 64, 8, 2, 64, 301},   {1, 64, 32, 8, 128, 302}, {1, 64, 40, 8, 128, 303},
+        {1, 64, 8, 1, 128, 304},  {1, 16, 1, 1, 256, 305},  {2, 64, 4, 4, 64, 400},
+        {2, 128, 4, 2, 128, 401}, {3, 33, 4, 4, 128, 402},  {2, 129, 32, 8, 128, 403},
+    };
+    std::printf("[prefill: the reference's 18 cases, synchronous launcher]\n");
+    for (const C& c : ref_cases)
+        if (!run_case(c.B, c.S, c.S, c.H_q, c.H_kv, c.D, c.seed, true)) ++failed;
+
+    std::printf("[decode and mixed q_len/kv_len, asynchronous launcher with Mi/Li]\n");
+    struct DC { int B, q_len, kv_len, H_q, H_kv, D; uint32_t seed; };
+    const DC dec_cases[] = {
+        {1, 1, 512, 32, 8, 128, 500},   {1, 1, 4096, 32, 8, 128, 501},
+        {1, 1, 2048, 32, 1, 64, 502},   {8, 1, 1024, 32, 8, 128, 503},
+        {2, 1, 1, 4, 2, 64, 504},       {1, 1, 33, 8, 1, 16, 505},
+        {1, 1, 1000, 4, 4, 256, 506},   {3, 2, 777, 8, 2, 128, 507},
+        {1, 16, 300, 8, 8, 64, 508},    {1, 40, 513, 16, 4, 128, 509},
+    };
+    for (const DC& c : dec_cases)
+        if (!run_case(c.B, c.q_len, c.kv_len, c.H_q, c.H_kv, c.D, c.seed, false)) ++failed;
+
+    if (failed) {
+        std::printf("%d test(s) FAILED\n", failed);
+        return EXIT_FAILURE;
+    }
+    std::printf("All flash-attention tests PASSED.\n");
+    return EXIT_SUCCESS;
+}

@@ -1,0 +1,173 @@
+"""The C ABI of libkf_attn.so, exercised without a GPU.
+
+Checks that the library loads, exports every function include/kf/attn.h
+declares, carries gfx950 code, plans the documented dispatch, and rejects
+every invalid argument with its status code before any HIP call (the fake
+device pointers below are never dereferenced).
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import kernelfoundry_amd as kf
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+FAKE = 0x10000          # 16-byte aligned, never dereferenced
+FAKE_WS = 0x20000       # 256-byte aligned
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return kf.load_library()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = kf.exported_symbols()
+    assert set(names) >= {"kf_attn_fwd", "kf_attn_plan", "kf_attn_workspace_bytes",
+                          "kf_launch_flash_attn", "kf_status_string", "kf_last_hip_error",
+                          "kf_version"}
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in kf/attn.h but not exported"
+    out = subprocess.run(["nm", "-D", "--defined-only", kf.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\s[TW]\s+(kf_\w+)$", out, re.M))
+    assert exported == set(names), f"undeclared exports: {exported - set(names)}"
+
+
+def test_library_carries_gfx950_code():
+    with open(kf.LIB_PATH, "rb") as f:
+        blob = f.read()
+    assert b"gfx950" in blob
+    for kern in (b"kf_attn_prefill_kernel", b"kf_attn_decode_kernel"):
+        assert kern in blob
+
+
+def test_version(lib):
+    assert b"gfx950" in lib.kf_version()
+
+
+def _fwd(B=1, q=4, kv=64, H_q=8, H_kv=2, D=128, Q=FAKE, K=FAKE, V=FAKE, O=FAKE, ws=None,
+         ws_bytes=0):
+    return kf.attn_fwd_ptr(Q, K, V, O, 0, 0, B, q, kv, H_q, H_kv, D, ws or 0, ws_bytes, 0)
+
+
+@pytest.mark.parametrize("D", [0, -1, 8, 32, 96, 100, 512])
+def test_bad_head_dim(D):
+    assert _fwd(D=D) == kf.KF_ERR_HEAD_DIM
+    assert kf.workspace_bytes(1, 1, 64, 8, 2, D) == 0
+
+
+@pytest.mark.parametrize("H_q,H_kv", [(8, 3), (5, 2), (1, 2)])
+def test_bad_gqa_ratio(H_q, H_kv):
+    assert _fwd(H_q=H_q, H_kv=H_kv) == kf.KF_ERR_GQA
+
+
+@pytest.mark.parametrize("field", ["B", "q", "kv", "H_q", "H_kv"])
+@pytest.mark.parametrize("value", [0, -3])
+def test_bad_sizes(field, value):
+    assert _fwd(**{field: value}) == kf.KF_ERR_SIZE
+
+
+def test_size_overflow_of_32bit_in_head_indexing():
+    assert _fwd(kv=(1 << 31) // 128 + 1, H_q=8, H_kv=8) == kf.KF_ERR_SIZE
+    assert _fwd(q=(1 << 31) // (128 * 4) + 1, H_q=8, H_kv=2) == kf.KF_ERR_SIZE
+
+
+@pytest.mark.parametrize("which", ["Q", "K", "V", "O"])
+def test_null_pointers(which):
+    assert _fwd(**{which: 0}) == kf.KF_ERR_NULL
+
+
+@pytest.mark.parametrize("which", ["Q", "K", "V", "O"])
+def test_misaligned_pointers(which):
+    assert _fwd(**{which: FAKE + 2}) == kf.KF_ERR_ALIGN
+
+
+def test_workspace_required_for_split_decode():
+    pl = kf.plan(1, 1, 4096, 32, 8, 128)
+    assert pl.path == "decode_split" and pl.workspace_bytes > 0
+    args = dict(B=1, q=1, kv=4096, H_q=32, H_kv=8, D=128)
+    assert _fwd(**args) == kf.KF_ERR_WORKSPACE
+    assert _fwd(ws=FAKE_WS, ws_bytes=pl.workspace_bytes - 1, **args) == kf.KF_ERR_WORKSPACE
+    assert _fwd(ws=FAKE_WS + 16, ws_bytes=pl.workspace_bytes, **args) == kf.KF_ERR_ALIGN
+
+
+def test_reference_launcher_rejects_like_the_reference():
+    # tests/test_flash_attn.cu:96-100: unsupported D -> cudaErrorInvalidValue.
+    assert kf.launch_flash_attn(FAKE, FAKE, FAKE, FAKE, 1, 64, 8, 2, 96) == kf.HIP_ERROR_INVALID_VALUE
+    assert kf.launch_flash_attn(FAKE, FAKE, FAKE, FAKE, 1, 64, 8, 3, 128) == kf.HIP_ERROR_INVALID_VALUE
+    assert kf.launch_flash_attn(0, FAKE, FAKE, FAKE, 1, 64, 8, 2, 128) == kf.HIP_ERROR_INVALID_VALUE
+
+
+def test_status_strings_distinct(lib):
+    texts = [kf.status_string(s) for s in range(8)]
+    assert len(set(texts)) == 8
+    assert kf.status_string(99) == "unknown status"
+
+
+def test_plan_null_out(lib):
+    assert lib.kf_attn_plan(1, 1, 1, 1, 1, 128, None) == kf.KF_ERR_NULL
+
+
+# ---------------------------------------------------------------------------
+# Dispatch plans for the BASELINE.json configs and the split geometry.
+# ---------------------------------------------------------------------------
+def test_plans_for_baseline_configs():
+    p = kf.plan(1, 4096, 4096, 32, 8, 128)           # C3 prefill
+    assert p.path == "prefill" and p.rows_per_group == 4 * 4096 and p.grid_blocks == 8 * 128
+    p = kf.plan(1, 512, 512, 32, 8, 128)             # C1
+    assert p.path == "prefill" and p.grid_blocks == 8 * 16 and p.workspace_bytes == 0
+    p = kf.plan(1, 1, 4096, 32, 8, 128)              # C2 decode
+    assert p.path == "decode_split" and p.rows_per_group == 4
+    p = kf.plan(1, 2048, 2048, 32, 1, 64)            # C4a MQA prefill
+    assert p.path == "prefill" and p.rows_per_group == 32 * 2048
+    p = kf.plan(1, 1, 2048, 32, 1, 64)               # C4b MQA decode
+    assert p.path == "decode_split" and p.rows_per_group == 32
+    p = kf.plan(32, 1, 8192, 32, 8, 128)             # C5 batched decode
+    assert p.path == "decode_split" and p.grid_blocks == 256 * p.num_splits
+
+
+@pytest.mark.parametrize("B,q,kv,H_q,H_kv,D", [
+    (1, 1, 1, 4, 1, 128), (1, 1, 31, 8, 8, 64), (1, 1, 129, 8, 8, 64), (2, 3, 1000, 8, 2, 16),
+    (1, 1, 100000, 32, 8, 128), (64, 1, 300, 32, 8, 256), (1, 8, 4000, 4, 1, 128),
+])
+def test_decode_split_geometry_covers_kv(B, q, kv, H_q, H_kv, D):
+    p = kf.plan(B, q, kv, H_q, H_kv, D)
+    assert p.rows_per_group == (H_q // H_kv) * q <= 32
+    assert p.kv_per_split % 32 == 0
+    assert (p.num_splits - 1) * p.kv_per_split < kv <= p.num_splits * p.kv_per_split
+    assert p.grid_blocks == B * H_kv * p.num_splits
+    if p.num_splits == 1:
+        assert p.path == "decode" and p.workspace_bytes == 0
+    else:
+        parts = B * H_q * q * p.num_splits
+        assert p.workspace_bytes >= parts * (D + 2) * 4 + B * H_kv * 8
+
+
+def test_prefill_threshold():
+    assert kf.plan(1, 8, 100, 4, 1, 128).path != "prefill"   # 32 rows per KV head
+    assert kf.plan(1, 9, 100, 4, 1, 128).path == "prefill"   # 36 rows
+
+
+# ---------------------------------------------------------------------------
+# Headers compile; the product never imports the oracle.
+# ---------------------------------------------------------------------------
+def test_c_header_compiles_as_c(tmp_path):
+    src = tmp_path / "t.c"
+    src.write_text('#include "kf/attn.h"\nint main(void){kf_attn_plan_t p; return kf_attn_plan(1,1,1,1,1,128,&p);}\n')
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only",
+                    f"-I{os.path.join(REPO, 'include')}", str(src)], check=True)
+
+
+def test_product_does_not_use_oracle():
+    pkg = os.path.join(REPO, "kernelfoundry_amd")
+    for root, _, files in os.walk(pkg):
+        for fn in files:
+            if fn.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(root, fn)).read()
+                assert "import oracle" not in text and "from oracle" not in text, fn
+                assert "cpu_attn" not in text and "kf_oracle" not in text, fn

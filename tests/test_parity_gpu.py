@@ -1,0 +1,255 @@
+"""GPU parity of the HIP attention kernels against the CPU oracle.
+
+Every case runs the gfx950 kernels through the C ABI (kf_attn_fwd /
+kf_launch_flash_attn in libkf_attn.so) on seeded fp16 inputs and compares
+with oracle/attn_oracle.py's fp64 attention on the same fp16 values.
+
+Tolerance: max |got - ref| <= 2e-3 AND
+||got - ref||_2 / ||ref||_2 <= 1e-2, for O.  Mi (max scaled score) to
+1e-4 absolute and Li (sum of exp) to 1e-3 relative.
+
+Large configs (S=4096 prefill, B=32 x KV=8192 decode) are checked exactly on
+sampled (b, h) heads plus size-independent properties on every head.
+"""
+import numpy as np
+import pytest
+
+from oracle import attn_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = orc.ATOL, orc.RTOL
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    return torch
+
+
+def _run_kf(q16, k16, v16):
+    """Upload fp16 numpy arrays, run kf_attn_fwd, return (O, Mi, Li) numpy."""
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    Q = torch.from_numpy(np.ascontiguousarray(q16)).cuda()
+    K = torch.from_numpy(np.ascontiguousarray(k16)).cuda()
+    V = torch.from_numpy(np.ascontiguousarray(v16)).cuda()
+    O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True)
+    torch.cuda.synchronize()
+    return O.cpu().numpy(), Mi.cpu().numpy(), Li.cpu().numpy()
+
+
+def _announce(**kw):
+    print("case", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _check(got, ref, label):
+    ok, max_abs, rel = orc.within_tolerance(got, ref)
+    assert np.isfinite(got).all(), f"{label}: non-finite output"
+    assert ok, f"{label}: max_abs={max_abs:.3g} rel={rel:.3g} (atol {ATOL}, rtol {RTOL})"
+    return max_abs, rel
+
+
+def _check_stats(Mi, Li, Mr, Lr, label):
+    assert np.abs(Mi - Mr).max() <= 1e-4, f"{label}: Mi off by {np.abs(Mi - Mr).max():.3g}"
+    rel = np.abs(Li - Lr).max() / np.abs(Lr).max()
+    assert rel <= 1e-3, f"{label}: Li rel err {rel:.3g}"
+
+
+# ---------------------------------------------------------------------------
+# The reference's 18 prefill cases (tests/test_flash_attn.cu:295-318), same
+# inputs (mt19937 U[-1,1], seeds s/s+1/s+2), through the reference-signature
+# synchronous launcher.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("case", orc.REFERENCE_CASES, ids=lambda c: "B{}_S{}_Hq{}_Hkv{}_D{}".format(*c))
+def test_reference_cases_sync_launcher(case):
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    B, S, H_q, H_kv, D, seed = case
+    _announce(B=B, S=S, H_q=H_q, H_kv=H_kv, D=D, seed=seed, entry="kf_launch_flash_attn")
+    (q, k, v), (q16, k16, v16) = orc.reference_case_inputs(B, S, H_q, H_kv, D, seed)
+    Q = torch.from_numpy(q16).cuda()
+    K = torch.from_numpy(k16).cuda()
+    V = torch.from_numpy(v16).cuda()
+    O = torch.full((B, H_q, S, D), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    err = kf.launch_flash_attn(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(),
+                               B, S, H_q, H_kv, D)
+    assert err == 0, f"hipError_t {err}"
+    got = O.cpu().numpy()
+    # The reference's own bar: fp32 attention on the unrounded inputs, 5e-2.
+    ref32, _, _ = orc.sdpa(q, k, v, acc=np.float32)
+    assert np.abs(got - ref32).max() <= orc.REFERENCE_TOL
+    # This library's bar: fp64 attention on the fp16 values the GPU saw.
+    ref64, _, _ = orc.sdpa(q16, k16, v16)
+    _check(got, ref64, f"ref case {case}")
+
+
+# ---------------------------------------------------------------------------
+# Prefill and decode shapes with Mi / Li, through the asynchronous entry.
+# ---------------------------------------------------------------------------
+SMALL_CASES = [
+    # (B, H_q, H_kv, q_len, kv_len, D, seed)
+    (1, 4, 1, 1, 1, 128, 11),        # kv_len = 1
+    (1, 8, 2, 1, 4096, 128, 12),     # decode, split
+    (2, 32, 8, 1, 512, 128, 13),     # batched decode
+    (1, 32, 1, 1, 2048, 64, 14),     # MQA decode, 32 rows per KV head
+    (1, 2, 2, 1, 100, 16, 15),       # D=16 decode, ragged
+    (1, 4, 4, 1, 333, 256, 16),      # D=256 decode, ragged
+    (1, 8, 8, 3, 1000, 64, 17),      # q_len=3 with MHA, R=3
+    (1, 4, 1, 8, 4000, 128, 18),     # R = 32 exactly
+    (1, 4, 1, 9, 257, 128, 19),      # R = 36 -> prefill path
+    (2, 8, 2, 200, 300, 128, 20),    # prefill q_len != kv_len
+    (1, 2, 1, 130, 70, 64, 21),      # prefill, ragged KV tile (BC=128 at D=64)
+    (1, 3, 1, 65, 65, 16, 22),       # D=16 prefill
+    (1, 2, 2, 40, 97, 256, 23),      # D=256 prefill
+    (1, 32, 8, 512, 512, 128, 1000), # BASELINE config C1 (S=512 GQA prefill)
+]
+
+
+@pytest.mark.parametrize("case", SMALL_CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_q{}_kv{}_D{}".format(*c[:6]))
+def test_parity_with_stats(case):
+    import kernelfoundry_amd as kf
+    B, H_q, H_kv, q_len, kv_len, D, seed = case
+    pl = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
+    _announce(B=B, H_q=H_q, H_kv=H_kv, q_len=q_len, kv_len=kv_len, D=D, seed=seed, path=pl.path,
+              splits=pl.num_splits)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, q_len, kv_len, D, seed)
+    O, Mi, Li = _run_kf(q16, k16, v16)
+    Or, Mr, Lr = orc.sdpa(q16, k16, v16)
+    _check(O, Or, str(case))
+    _check_stats(Mi, Li, Mr, Lr, str(case))
+
+
+@pytest.mark.parametrize("q_len", [1, 5, 40])
+def test_kv_len_one_returns_v0(q_len):
+    """KV_len = 1: the softmax weight is 1, so O = V_0 and Li = 1.
+
+    The kernels exponentiate exp2(fma(s, c, -m)) with m = round(s_max * c),
+    so the max term is exp2 of the fma's rounding residual (|.| <= half an
+    ulp of m), and O is scaled by a rounded reciprocal of the row sum: O and
+    Li equal V_0 and 1 to within 4 ulp (5e-7 relative), not bit-exactly."""
+    B, H_q, H_kv, D = 2, 8, 2, 128
+    _announce(test="kv_len_one", B=B, H_q=H_q, H_kv=H_kv, q_len=q_len, D=D)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, q_len, 1, D, 77)
+    O, Mi, Li = _run_kf(q16, k16, v16)
+    expect = np.repeat(v16.astype(np.float32), H_q // H_kv, axis=1)
+    expect = np.broadcast_to(expect, O.shape)
+    np.testing.assert_allclose(O, expect, rtol=5e-7, atol=0)
+    np.testing.assert_allclose(Li, np.ones_like(Li), rtol=5e-7, atol=0)
+
+
+def test_decode_split_matches_unsplit_prefill_rows():
+    """The same query rows through the split-KV decode path and the prefill
+    path (forced by q_len > 32 rows) agree to well inside tolerance."""
+    import kernelfoundry_amd as kf
+    B, H_q, H_kv, kv_len, D = 1, 4, 1, 3000, 128
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 16, kv_len, D, 31)
+    assert kf.plan(B, 16, kv_len, H_q, H_kv, D).path == "prefill"
+    assert kf.plan(B, 8, kv_len, H_q, H_kv, D).path == "decode_split"
+    _announce(test="split_vs_prefill", kv_len=kv_len)
+    O16, M16, L16 = _run_kf(q16, k16, v16)
+    O8, M8, L8 = _run_kf(np.ascontiguousarray(q16[:, :, :8]), k16, v16)
+    assert np.abs(O16[:, :, :8] - O8).max() < 1e-4
+    assert np.abs(M16[:, :, :8] - M8).max() < 1e-5
+
+
+def test_gqa_equals_mha_with_repeated_kv():
+    """GQA output equals MHA on repeat_interleave'd K/V (the comparator's
+    expansion, reference_benchmarks/bench_flash_attn2.py:56-57)."""
+    B, H_q, H_kv, S, D = 1, 8, 2, 192, 64
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, S, S, D, 41)
+    _announce(test="gqa_vs_mha", S=S)
+    O_g, _, _ = _run_kf(q16, k16, v16)
+    r = H_q // H_kv
+    O_m, _, _ = _run_kf(q16, np.repeat(k16, r, axis=1), np.repeat(v16, r, axis=1))
+    assert np.array_equal(O_g, O_m)
+
+
+# ---------------------------------------------------------------------------
+# BASELINE.json configs at full size.
+# ---------------------------------------------------------------------------
+def _property_checks(O, Mi, Li, v16, H_q, H_kv):
+    assert np.isfinite(O).all() and np.isfinite(Mi).all() and np.isfinite(Li).all()
+    assert (Li >= 1.0 - 1e-5).all()  # the max term contributes exactly 1
+    # Each output row is a convex combination of V rows: per-column bounds.
+    r = H_q // H_kv
+    vmin = np.repeat(v16.astype(np.float32).min(axis=2), r, axis=1)[:, :, None, :]
+    vmax = np.repeat(v16.astype(np.float32).max(axis=2), r, axis=1)[:, :, None, :]
+    assert (O >= vmin - 1e-3).all() and (O <= vmax + 1e-3).all()
+
+
+def _sampled_heads_check(O, Mi, Li, q16, k16, v16, heads):
+    for b, h in heads:
+        H_q, H_kv = q16.shape[1], k16.shape[1]
+        hk = h // (H_q // H_kv)
+        Or, Mr, Lr = orc.sdpa(q16[b:b + 1, h:h + 1], k16[b:b + 1, hk:hk + 1], v16[b:b + 1, hk:hk + 1])
+        _check(O[b:b + 1, h:h + 1], Or, f"head b={b} h={h}")
+        _check_stats(Mi[b:b + 1, h:h + 1], Li[b:b + 1, h:h + 1], Mr, Lr, f"head b={b} h={h}")
+
+
+@pytest.mark.parametrize("S", [1024, 2048, 4096])
+def test_config_c3_gqa_prefill(S):
+    B, H_q, H_kv, D = 1, 32, 8, 128
+    _announce(config="C3", S=S)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, S, S, D, 3000)
+    O, Mi, Li = _run_kf(q16, k16, v16)
+    _property_checks(O, Mi, Li, v16, H_q, H_kv)
+    _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (0, 13), (0, 31)])
+
+
+def test_config_c2_gqa_decode():
+    B, H_q, H_kv, D, kv = 1, 32, 8, 128, 4096
+    _announce(config="C2", kv=kv)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 1, kv, D, 2000)
+    O, Mi, Li = _run_kf(q16, k16, v16)
+    Or, Mr, Lr = orc.sdpa(q16, k16, v16)
+    _check(O, Or, "C2")
+    _check_stats(Mi, Li, Mr, Lr, "C2")
+
+
+def test_config_c4_mqa_d64():
+    B, H_q, H_kv, D, S = 1, 32, 1, 64, 2048
+    _announce(config="C4a", S=S)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, S, S, D, 4000)
+    O, Mi, Li = _run_kf(q16, k16, v16)
+    _property_checks(O, Mi, Li, v16, H_q, H_kv)
+    _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (0, 17), (0, 31)])
+    _announce(config="C4b", kv=S)
+    q1 = np.ascontiguousarray(q16[:, :, :1])
+    O1, M1, L1 = _run_kf(q1, k16, v16)
+    Or, Mr, Lr = orc.sdpa(q1, k16, v16)
+    _check(O1, Or, "C4b")
+    _check_stats(M1, L1, Mr, Lr, "C4b")
+
+
+def test_config_c5_batched_long_decode():
+    B, H_q, H_kv, D, kv = 32, 32, 8, 128, 8192
+    _announce(config="C5", B=B, kv=kv)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 1, kv, D, 5000)
+    O, Mi, Li = _run_kf(q16, k16, v16)
+    _property_checks(O, Mi, Li, v16, H_q, H_kv)
+    _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (7, 9), (31, 31), (16, 4)])
+
+
+def test_split_merge_needs_no_workspace_init():
+    """The fused split merge takes (epoch, count) tickets in the workspace:
+    a workspace full of garbage, and one reused across calls, must both give
+    the oracle's answer (a count left by another call restarts at 1)."""
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    B, H_q, H_kv, kv_len, D = 2, 16, 4, 2500, 128
+    pl = kf.plan(B, 1, kv_len, H_q, H_kv, D)
+    assert pl.path == "decode_split" and pl.num_splits > 1
+    _announce(test="split_ws_garbage", B=B, kv_len=kv_len, splits=pl.num_splits)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 1, kv_len, D, 61)
+    Or, Mr, Lr = orc.sdpa(q16, k16, v16)
+    Q = torch.from_numpy(q16).cuda()
+    K = torch.from_numpy(k16).cuda()
+    V = torch.from_numpy(v16).cuda()
+    ws = torch.randint(0, 256, (pl.workspace_bytes,), dtype=torch.uint8, device="cuda")
+    for it in range(3):
+        O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True, workspace=ws)
+        torch.cuda.synchronize()
+        _check(O.cpu().numpy(), Or, f"iteration {it}")
+        _check_stats(Mi.cpu().numpy(), Li.cpu().numpy(), Mr, Lr, f"iteration {it}")
