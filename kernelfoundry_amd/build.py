@@ -22,10 +22,14 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # Packed-fp32 VALU ops are kept out of every code object (-packed-fp32-ops).
+# -fno-honor-nans lets fmaxf skip NaN canonicalisation of MFMA results (the
+# kernels never produce or test NaN); infinities keep their IEEE meaning,
+# which the -inf score masking relies on.
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
+    "-fno-honor-nans",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

@@ -5,7 +5,6 @@
 // CPU-only tests rely on that) and never reach a kernel.
 #include <hip/hip_runtime.h>
 
-#include <atomic>
 #include <climits>
 #include <cstdint>
 #include <cstdio>
@@ -23,13 +22,7 @@ constexpr int kDecodeMinSplitRows = 4 * kf::kDecodeStage;  // one stage per wave
 constexpr size_t kWsAlign = 256;
 
 thread_local int g_last_hip_error = 0;
-std::atomic<unsigned> g_epoch{0};  // split-merge ticket epochs, unique per call
 
-unsigned next_epoch() {
-    unsigned e = g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
-    if (e == 0u) e = g_epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
-    return e;
-}
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -45,7 +38,7 @@ struct Plan {
     int grid;
     int threads;
     size_t ws_bytes;
-    size_t ws_o_off, ws_m_off, ws_l_off, ws_t_off;
+    size_t ws_o_off, ws_m_off, ws_l_off;
 };
 
 int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) {
@@ -68,6 +61,7 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) 
         long long splits = (kDecodeTargetBlocks + n_groups - 1) / n_groups;
         const long long max_splits = (kv_len + kDecodeMinSplitRows - 1) / kDecodeMinSplitRows;
         if (splits > max_splits) splits = max_splits;
+        if (splits > kf::kMergeMaxSplits) splits = kf::kMergeMaxSplits;
         if (splits < 1) splits = 1;
         long long per = (kv_len + splits - 1) / splits;
         per = (per + kf::kDecodeStage - 1) / kf::kDecodeStage * kf::kDecodeStage;
@@ -92,8 +86,7 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) 
         p.ws_o_off = 0;
         p.ws_m_off = align_up(parts * D * sizeof(float), kWsAlign);
         p.ws_l_off = p.ws_m_off + align_up(parts * sizeof(float), kWsAlign);
-        p.ws_t_off = p.ws_l_off + align_up(parts * sizeof(float), kWsAlign);
-        p.ws_bytes = p.ws_t_off + align_up((size_t)n_groups * sizeof(unsigned long long), kWsAlign);
+        p.ws_bytes = p.ws_l_off + align_up(parts * sizeof(float), kWsAlign);
     }
     *pl = p;
     return KF_OK;
@@ -113,6 +106,9 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
         return hipGetLastError();
     }
     kf::kf_attn_decode_kernel<D><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || pl.path != KF_PATH_DECODE_SPLIT) return e;
+    kf::kf_attn_split_merge_kernel<D><<<dim3(pl.rows_total), dim3(kf::kMergeThreads), 0, stream>>>(prm);
     return hipGetLastError();
 }
 
@@ -166,8 +162,6 @@ int kf_attn_fwd(const void* Q, const void* K, const void* V, float* O, float* ro
         prm.Opart = reinterpret_cast<float*>(ws + pl.ws_o_off);
         prm.Mpart = reinterpret_cast<float*>(ws + pl.ws_m_off);
         prm.Lpart = reinterpret_cast<float*>(ws + pl.ws_l_off);
-        prm.tickets = reinterpret_cast<unsigned long long*>(ws + pl.ws_t_off);
-        prm.epoch = next_epoch();
     }
     prm.rows_per_group = pl.R;
     prm.kv_len = kv_len;

@@ -1,6 +1,6 @@
 // attn_kernels.h -- gfx950 (CDNA4) flash-attention forward kernels.
 //
-// Two kernels, both hand-written for wave64 and the fp16 MFMA
+// Three kernels, all hand-written for wave64 and the fp16 MFMA
 // v_mfma_f32_32x32x16_f16:
 //
 //   kf_attn_prefill_kernel<D>  one workgroup = 4 waves = 128 query rows of one
@@ -11,10 +11,8 @@
 //                              groups): every wave streams its own KV stages
 //                              through a wave-private LDS slot; the 4 waves of
 //                              a workgroup merge in LDS; with several splits
-//                              each workgroup writes an unnormalised partial
-//                              and the last one of its group to finish merges
-//                              them into O, Mi, Li (one launch, no combine
-//                              kernel).
+//                              each workgroup writes an unnormalised partial.
+//   kf_attn_split_merge_kernel<D>  merges the split partials into O, Mi, Li.
 //
 // Behaviour follows the reference forward (kernels/flash_attn.cu:384-585):
 // O = softmax(Q K^T / sqrt(D)) V per (b, h_q) with h_kv = h_q / (H_q / H_kv)
@@ -52,6 +50,7 @@ namespace kf {
 typedef _Float16 f16;
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -78,8 +77,6 @@ struct AttnParams {
     float* Opart;       // split partials [B * H_kv][n_splits][R][D], unnormalised
     float* Mpart;       // [B * H_kv][n_splits][R]  max of scaled scores
     float* Lpart;       // [B * H_kv][n_splits][R]  sum of exp relative to Mpart
-    unsigned long long* tickets;  // [B * H_kv] split-merge tickets (epoch << 32 | count)
-    unsigned epoch;     // unique per call, never 0
     int rows_per_group; // R = (H_q / H_kv) * q_len
     int kv_len;
     int row_tiles;      // prefill: ceil(R / 128)
@@ -114,25 +111,6 @@ __device__ __forceinline__ int xcd_remap(int hw, int n) {
     const int q = n / kXcds, r = n % kXcds;
     const int xcd = hw % kXcds, k = hw / kXcds;
     return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + k;
-}
-
-// Count this workgroup into its group's split merge; true for the last of
-// n arrivals in this call.  The word holds (epoch << 32 | count): a count
-// left by an earlier call (other epoch) restarts at 1, so the workspace needs
-// no zeroing between calls.  Every failed compare-and-swap means another
-// workgroup's swap succeeded; with n arrivals per epoch the loop ends after
-// at most n iterations.
-__device__ __forceinline__ bool take_ticket(unsigned long long* word, unsigned epoch, int n) {
-    unsigned long long old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    unsigned cnt;
-    for (;;) {
-        const unsigned long long assumed = old;
-        cnt = (unsigned)(assumed >> 32) == epoch ? (unsigned)(assumed & 0xffffffffu) + 1u : 1u;
-        const unsigned long long want = ((unsigned long long)epoch << 32) | cnt;
-        old = atomicCAS(word, assumed, want);
-        if (old == assumed) break;
-    }
-    return cnt == (unsigned)n;
 }
 
 // Order LDS traffic between the lanes of one wave (wave-private buffers).
@@ -281,8 +259,11 @@ struct RowState {
 };
 
 // Online-softmax update for NSB score blocks: moves the running max (lazily),
-// rescales O, exponentiates, accumulates the fp32 row sum and packs fp16 P^T
-// operands (p[j] covers kv 16j .. 16j+15 of the stage).
+// rescales O, exponentiates, packs fp16 P^T operands (p[j] covers kv
+// 16j .. 16j+15 of the stage) and accumulates the row sum of those fp16 P
+// values with v_dot2_f32_f16 (fp32 accumulation, two terms per instruction).
+// Summing the rounded P keeps numerator and denominator on the same weights;
+// it differs from a sum of the fp32 P by at most 2^-12 relative.
 template <int NSB, int NTD>
 __device__ __forceinline__ void softmax_update(f32x16 (&s)[NSB], RowState& st,
                                                f32x16 (&o)[NTD], float scale_log2,
@@ -305,21 +286,24 @@ __device__ __forceinline__ void softmax_update(f32x16 (&s)[NSB], RowState& st,
         st.m = mnew;
     }
     const float neg_m = -st.m;
-    float sum = 0.f;
+    const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+    float sum[2] = {0.f, 0.f};
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             f32x8 e;
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                e[r] = exp2_hw(fmaf(s[sb][8 * h + r], scale_log2, neg_m));
-                sum += e[r];
-            }
-            p[2 * sb + h] = __builtin_convertvector(e, f16x8);
+            for (int r = 0; r < 8; ++r) e[r] = exp2_hw(fmaf(s[sb][8 * h + r], scale_log2, neg_m));
+            const f16x8 ph = __builtin_convertvector(e, f16x8);
+            p[2 * sb + h] = ph;
+            sum[h] = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 0, 1), ones, sum[h], false);
+            sum[h] = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 2, 3), ones, sum[h], false);
+            sum[h] = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 4, 5), ones, sum[h], false);
+            sum[h] = __builtin_amdgcn_fdot2(__builtin_shufflevector(ph, ph, 6, 7), ones, sum[h], false);
         }
     }
-    st.l += sum;
+    st.l += sum[0] + sum[1];
 }
 
 // O^T += V^T . P^T over NJ 16-row kv steps of a V^T stage, starting at kv
@@ -345,97 +329,261 @@ __device__ __forceinline__ void pv_accum(const f16* __restrict__ Vt, int kv0,
 }
 
 // ---------------------------------------------------------------------------
-// Prefill: 4 waves x 32 query rows per workgroup, BC-row K/V stages shared by
-// all 4 waves, double-buffered in LDS with register-staged prefetch.
+// Prefill: 4 waves x 32 query rows per workgroup.  K and V stages of BC rows
+// are copied HBM -> LDS by the gfx950 LDS-DMA loads (global_load_lds_dwordx4:
+// each wave instruction fills one contiguous KiB of LDS, no VGPR staging),
+// double-buffered in two named LDS arrays so the prefetch of stage t+1
+// overlaps the MFMA/softmax work on stage t.  Both K and V stay row-major in
+// LDS with the 16-byte chunks of a row XOR-permuted by SwizzleRow<D>: K
+// fragments are read with ds_read_b128, and the V^T fragments of the P.V
+// MFMA with the transposing ds_read_b64_tr_b16, so V is never transposed by
+// VALU work.
 // ---------------------------------------------------------------------------
+
+// Row-dependent XOR applied to the 16-byte chunk index of a K / V row in LDS.
+// It depends only on row & 15, is a bijection on those 16 rows, and was
+// chosen (exhaustive search over GF(2)-linear maps) so that both access
+// patterns are bank-conflict-free with 32 or with 64 four-byte banks:
+//   ds_read_b128 of a 16-byte chunk column over 32 consecutive rows (K), and
+//   ds_read_b64_tr_b16 of 4 consecutive rows x 32 bytes per 16 lanes (V).
+template <int D> struct SwizzleRow;
+template <> struct SwizzleRow<16> {
+    static __device__ __forceinline__ int h(int row) { return row & 1; }
+};
+template <> struct SwizzleRow<64> {
+    static __device__ __forceinline__ int h(int row) {
+        const int r0 = row & 1, r1 = (row >> 1) & 1, r2 = (row >> 2) & 1, r3 = (row >> 3) & 1;
+        return r1 | ((r0 ^ r2) << 1) | ((r0 ^ r1 ^ r3) << 2);
+    }
+};
+template <> struct SwizzleRow<128> {
+    static __device__ __forceinline__ int h(int row) { const int r = row & 15; return r ^ ((r & 3) << 2); }
+};
+template <> struct SwizzleRow<256> : SwizzleRow<128> {};
+
 template <int D> struct PrefillCfg;
 template <> struct PrefillCfg<16>  { static constexpr int BC = 64;  static constexpr int kWavesPerEU = 2; };
 template <> struct PrefillCfg<64>  { static constexpr int BC = 128; static constexpr int kWavesPerEU = 2; };
 template <> struct PrefillCfg<128> { static constexpr int BC = 64;  static constexpr int kWavesPerEU = 2; };
 template <> struct PrefillCfg<256> { static constexpr int BC = 32;  static constexpr int kWavesPerEU = 1; };
 
-constexpr int kPrefillThreads = 256;
-constexpr int kPrefillRows = 128;
+constexpr int kPrefillWaves = 8;                  // waves per workgroup, 32 query rows each
+constexpr int kPrefillThreads = 64 * kPrefillWaves;
+constexpr int kPrefillRows = 32 * kPrefillWaves;
+
+template <int D, int BC>
+struct DmaStage {
+    static constexpr int kRowBytes = D * 2;
+    static constexpr int kChunks = D / 8;                        // 16-byte chunks per row
+    static constexpr int kRowsPerInstr = 1024 / kRowBytes;       // rows per wave instruction
+    static constexpr int kInstrPerTensor = BC * kRowBytes / 1024;
+    static constexpr int kInstrTotal = 2 * kInstrPerTensor;      // K instructions, then V
+    static constexpr int kPerWave = (kInstrTotal + kPrefillWaves - 1) / kPrefillWaves;
+    static constexpr int kTensorBytes = BC * kRowBytes;
+    static constexpr int kStageBytes = 2 * kTensorBytes;         // K region, then V region
+    static_assert(kRowsPerInstr * kRowBytes == 1024, "row size must divide 1 KiB");
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ f16x4 lds_read_tr16(const char* lds_byte_ptr) {
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_i16x4*)(const_cast<char*>(lds_byte_ptr)));
+    return __builtin_bit_cast(f16x4, v);
+}
 
 template <int D>
 __global__ __launch_bounds__(kPrefillThreads, PrefillCfg<D>::kWavesPerEU)
 void kf_attn_prefill_kernel(AttnParams p) {
     constexpr int BC = PrefillCfg<D>::BC;
-    using G = StageGeom<D, BC>;
-    __shared__ __attribute__((aligned(16))) f16 smem[2 * G::kStageHalfs];
+    using S = DmaStage<D, BC>;
+    using SW = SwizzleRow<D>;
+    constexpr int kNSB = BC / 32;                 // 32-row score blocks per stage
+    constexpr int kNKK = D / 16;                  // MFMA k-steps over D
+    constexpr int kNTD = (D < 32 ? 32 : D) / 32;  // 32-row O^T tiles
+    constexpr int kNJ = BC / 16;                  // P.V k-steps per stage
+    __shared__ __attribute__((aligned(1024))) char stage0[S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char stage1[S::kStageBytes];
+    __shared__ __attribute__((aligned(16))) char zero_pad[16];  // D=16: V^T rows 16..31
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
     const int rt = blk % p.row_tiles;
     const int grp = blk / p.row_tiles;
     const int R = p.rows_per_group;
     const int kv_len = p.kv_len;
+    const int ntiles = (kv_len + BC - 1) / BC;
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
-    const uint16_t* Kh = p.K + (size_t)grp * kv_len * D;
-    const uint16_t* Vh = p.V + (size_t)grp * kv_len * D;
+    const char* Kh = reinterpret_cast<const char*>(p.K + (size_t)grp * kv_len * D);
+    const char* Vh = reinterpret_cast<const char*>(p.V + (size_t)grp * kv_len * D);
 
-    const int row = rt * kPrefillRows + wave * 32 + (lane & 31);
-    f16x8 qf[D / 16];
-    load_q_frags<D>(Qg, row, R, lane, qf);
-
-    if constexpr (D < 32) {
-        // V^T rows D..31 pad the MFMA M dimension; keep them zero.
-        for (int i = tid; i < 2 * (32 - D) * G::kVtStride; i += kPrefillThreads) {
-            const int b = i / ((32 - D) * G::kVtStride);
-            const int j = i % ((32 - D) * G::kVtStride);
-            smem[b * G::kStageHalfs + G::kKHalfs + D * G::kVtStride + j] = (f16)0.f;
+    // ---- LDS-DMA copy plan: this wave issues instructions j = wave + W i. ----
+    // Lane l of instruction j writes LDS bytes [16 l, 16 l + 16) of KiB
+    // ii = (j mod kInstrPerTensor) of the K (j < kInstrPerTensor) or V region,
+    // i.e. row r = ii * kRowsPerInstr + l / kChunks, physical chunk
+    // l % kChunks, which holds logical chunk (l % kChunks) ^ h(r) of kv row r.
+    // lane_base[i]: byte offset of lane l's source chunk relative to the
+    // first row of instruction i (identical for all i unless D = 256).
+    uint32_t lane_base[S::kPerWave];
+#pragma unroll
+    for (int i = 0; i < S::kPerWave; ++i) {
+        const int ii = (wave + kPrefillWaves * i) % S::kInstrPerTensor;
+        const int lr = lane / S::kChunks;
+        const int r = ii * S::kRowsPerInstr + lr;
+        lane_base[i] = (uint32_t)(lr * S::kRowBytes +
+                                  (((lane % S::kChunks) ^ SW::h(r)) % S::kChunks) * 16);
+    }
+    auto issue_stage = [&](char* dst, int kv0) {
+        if (kv0 + BC <= kv_len) {
+            // Full stage: wave-uniform row base (SGPRs) + the lane's constant
+            // 32-bit offset; no per-lane address arithmetic.
+#pragma unroll
+            for (int i = 0; i < S::kPerWave; ++i) {
+                const int j = wave + kPrefillWaves * i;
+                if (S::kInstrTotal % kPrefillWaves == 0 || j < S::kInstrTotal) {
+                    const bool is_v = j >= S::kInstrPerTensor;
+                    const int ii = j % S::kInstrPerTensor;
+                    const char* base = (is_v ? Vh : Kh) +
+                                       (size_t)(kv0 + ii * S::kRowsPerInstr) * S::kRowBytes;
+                    char* d = dst + (is_v ? S::kTensorBytes : 0) + ii * 1024;
+                    // Keep the 32-bit lane offset opaque so the address stays
+                    // "SGPR base + VGPR offset" instead of a hoisted 64-bit sum.
+                    uint32_t lb = lane_base[i];
+                    asm volatile("" : "+v"(lb));
+                    __builtin_amdgcn_global_load_lds(base + lb, (lds_void*)d, 16, 0, 0);
+                }
+            }
+        } else {
+            // Last, partial stage: rows past kv_len re-read row kv_len - 1
+            // (finite data whose scores are masked to -inf, so P = 0).
+            asm volatile("" ::: "memory");
+            const int lr = lane / S::kChunks;
+#pragma unroll
+            for (int i = 0; i < S::kPerWave; ++i) {
+                const int j = wave + kPrefillWaves * i;
+                if (S::kInstrTotal % kPrefillWaves == 0 || j < S::kInstrTotal) {
+                    const bool is_v = j >= S::kInstrPerTensor;
+                    const int ii = j % S::kInstrPerTensor;
+                    const int kv = min(kv0 + ii * S::kRowsPerInstr + lr, kv_len - 1);
+                    const uint32_t off = (uint32_t)kv * S::kRowBytes +
+                                         (lane_base[i] - (uint32_t)(lr * S::kRowBytes));
+                    char* d = dst + (is_v ? S::kTensorBytes : 0) + ii * 1024;
+                    __builtin_amdgcn_global_load_lds((is_v ? Vh : Kh) + off, (lds_void*)d, 16, 0, 0);
+                }
+            }
         }
+    };
+
+    // ---- Per-lane LDS read offsets (bytes within a stage). ----
+    // K (A of S^T = K Q^T): row l%32 (+32 sb), logical chunk 2 kk + g.
+    int koff[kNKK];
+#pragma unroll
+    for (int kk = 0; kk < kNKK; ++kk) {
+        const int r = lane & 31;
+        koff[kk] = r * S::kRowBytes + (((2 * kk + g) ^ SW::h(r)) % S::kChunks) * 16;
+    }
+    // V (A of O^T += V^T P^T) via ds_read_b64_tr_b16: 16-lane group G = l/16,
+    // w = l%16 supplies row 4 (G/2) + w/4 (+8 for the second half of the
+    // 16-row k step) and the 8 bytes at d = 32 td + 16 (G%2) + 4 (w%4).
+    int voff[kNTD][2];
+    {
+        const int G = lane >> 4, w = lane & 15;
+#pragma unroll
+        for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int r = 4 * (G >> 1) + (w >> 2) + 8 * h2;
+                const int d = 32 * td + 16 * (G & 1) + 4 * (w & 3);
+                if (d < D) {
+                    const int c = d >> 3, half = (d >> 2) & 1;
+                    voff[td][h2] = S::kTensorBytes + r * S::kRowBytes +
+                                   ((c ^ SW::h(r)) % S::kChunks) * 16 + half * 8;
+                } else {
+                    voff[td][h2] = -1;  // D=16 padding rows of V^T: read zeros
+                }
+            }
     }
 
-    StageLoader<D, BC, kPrefillThreads> ld;
-    const int ntiles = (kv_len + BC - 1) / BC;
-    ld.load(Kh, Vh, 0, kv_len, tid);
-    ld.store(smem, smem + G::kKHalfs, tid);
+    // ---- Prologue: stage 0 and the query fragments. ----
+    issue_stage(stage0, 0);
+    const int row = rt * kPrefillRows + wave * 32 + (lane & 31);
+    f16x8 qf[kNKK];
+    load_q_frags<D>(Qg, row, R, lane, qf);
+    if constexpr (D < 32) {
+        if (tid < 4) reinterpret_cast<uint32_t*>(zero_pad)[tid] = 0u;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
     RowState st{-INFINITY, -INFINITY, 0.f};
-    f32x16 o[G::kNTD];
+    f32x16 o[kNTD];
 #pragma unroll
-    for (int td = 0; td < G::kNTD; ++td) o[td] = f32x16{};
+    for (int td = 0; td < kNTD; ++td) o[td] = f32x16{};
 
-    for (int t = 0; t < ntiles; ++t) {
-        const f16* Ks = smem + (t & 1) * G::kStageHalfs;
-        const f16* Vt = Ks + G::kKHalfs;
-        if (t + 1 < ntiles) ld.load(Kh, Vh, (t + 1) * BC, kv_len, tid);
-
-        f32x16 s[G::kNSB];
+    auto compute_stage = [&](const char* cur, int t) {
+        f32x16 s[kNSB];
 #pragma unroll
-        for (int sb = 0; sb < G::kNSB; ++sb) s[sb] = qk_block<D, BC>(Ks, 32 * sb, qf, lane);
+        for (int sb = 0; sb < kNSB; ++sb) {
+            f16x8 kf[kNKK];
+#pragma unroll
+            for (int kk = 0; kk < kNKK; ++kk)
+                kf[kk] = *reinterpret_cast<const f16x8*>(cur + koff[kk] + sb * 32 * S::kRowBytes);
+            s[sb] = f32x16{};
+#pragma unroll
+            for (int kk = 0; kk < kNKK; ++kk) s[sb] = mfma32(kf[kk], qf[kk], s[sb]);
+        }
         if ((t + 1) * BC > kv_len) {
             const int lim = kv_len - t * BC;
 #pragma unroll
-            for (int sb = 0; sb < G::kNSB; ++sb)
+            for (int sb = 0; sb < kNSB; ++sb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     if (32 * sb + acc_row(r, lane) >= lim) s[sb][r] = -INFINITY;
         }
-        f16x8 pb[2 * G::kNSB];
-        softmax_update<G::kNSB, G::kNTD>(s, st, o, p.scale_log2, pb);
-        pv_accum<D, BC, 2 * G::kNSB>(Vt, 0, pb, o, lane);
+        f16x8 pb[kNJ];
+        softmax_update<kNSB, kNTD>(s, st, o, p.scale_log2, pb);
+#pragma unroll
+        for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+            for (int jj = 0; jj < kNJ; ++jj) {
+                f16x4 lo, hi;
+                if (D < 32 && voff[td][0] < 0) {
+                    lo = lds_read_tr16(zero_pad);
+                    hi = lo;
+                } else {
+                    lo = lds_read_tr16(cur + voff[td][0] + jj * 16 * S::kRowBytes);
+                    hi = lds_read_tr16(cur + voff[td][1] + jj * 16 * S::kRowBytes);
+                }
+                const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                o[td] = mfma32(a, pb[jj], o[td]);
+            }
+    };
 
-        if (t + 1 < ntiles) {
-            f16* Kn = smem + ((t + 1) & 1) * G::kStageHalfs;
-            ld.store(Kn, Kn + G::kKHalfs, tid);
-        }
+    for (int t = 0; t < ntiles; t += 2) {
+        if (t + 1 < ntiles) issue_stage(stage1, (t + 1) * BC);
+        compute_stage(stage0, t);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t + 1 >= ntiles) break;
+        if (t + 2 < ntiles) issue_stage(stage0, (t + 2) * BC);
+        compute_stage(stage1, t + 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
 
-    // Epilogue: combine the two half-row partial sums, normalise, store.
+    // ---- Epilogue: combine the two half-row partial sums, normalise, store. ----
     const float l = st.l + __shfl_xor(st.l, 32);
     if (row < R) {
         const float inv = 1.0f / l;
         float* Orow = p.O + ((size_t)grp * R + row) * D;
 #pragma unroll
-        for (int td = 0; td < G::kNTD; ++td)
+        for (int td = 0; td < kNTD; ++td)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int d = 32 * td + 8 * i + 4 * g;
@@ -608,44 +756,85 @@ void kf_attn_decode_kernel(AttnParams p) {
             }
         }
     }
-    if (p.n_splits == 1) return;
+}
 
-    // Split-KV merge, fused: the last workgroup of this group to finish merges
-    // every split's partial.  Release the partials device-wide (other XCDs'
-    // L2s included), then take a ticket.
-    __threadfence();
+// ---------------------------------------------------------------------------
+// Split merge: one workgroup per query row.  Phase 1 stages every split's
+// (M_k, l_k) for the row in LDS and turns them into weights
+// w_k = exp(M_k - max_k M_k); phase 2 spreads the splits over kLanes groups
+// of threads (each thread owns 4 consecutive d for splits k = lane, lane +
+// kLanes, ...) so every thread has only a few independent loads in flight,
+// then reduces the kLanes partial sums in LDS.
+//   O = sum_k w_k O_k / sum_k w_k l_k,  Mi = max_k M_k,  Li = sum_k w_k l_k.
+// ---------------------------------------------------------------------------
+constexpr int kMergeThreads = 256;
+constexpr int kMergeMaxSplits = 1024;
+
+template <int D>
+__global__ __launch_bounds__(kMergeThreads)
+void kf_attn_split_merge_kernel(AttnParams p) {
+    constexpr int kD4 = D / 4;                     // float4 columns per row
+    constexpr int kLanes = kMergeThreads / kD4;    // split lanes
+    __shared__ float s_w[kMergeMaxSplits];
+    __shared__ float s_red[kMergeThreads / 64];
+    __shared__ f32x4 s_acc[kLanes][kD4];
+
+    const int tid = threadIdx.x;
+    const int row = blockIdx.x;                    // global query row
+    const int R = p.rows_per_group;
+    const int grp = row / R, r = row % R;
+    const int ns = p.n_splits;
+    const size_t base = (size_t)grp * ns * R + r;  // partial index of split 0
+
+    // Phase 1: max over splits.
+    float m = -INFINITY;
+    for (int k = tid; k < ns; k += kMergeThreads) {
+        const float mk = p.Mpart[base + (size_t)k * R];
+        s_w[k] = mk;
+        m = fmaxf(m, mk);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((tid & 63) == 0) s_red[tid >> 6] = m;
     __syncthreads();
-    __shared__ int s_last;
-    if (tid == 0) s_last = take_ticket(p.tickets + grp, p.epoch, p.n_splits);
+    m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float lsum = 0.f;
+    for (int k = tid; k < ns; k += kMergeThreads) {
+        const float w = exp2_hw((s_w[k] - m) * kLog2e);
+        s_w[k] = w;
+        lsum += w * p.Lpart[base + (size_t)k * R];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off);
+    __syncthreads();  // s_red reuse; s_w complete
+    if ((tid & 63) == 0) s_red[tid >> 6] = lsum;
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();  // acquire: the other splits' partials are visible
-    if (mrow < R) {
-        const float* Mg = p.Mpart + (size_t)grp * p.n_splits * R + mrow;
-        const float* Lg = p.Lpart + (size_t)grp * p.n_splits * R + mrow;
-        const float* Og = p.Opart + ((size_t)grp * p.n_splits * R + mrow) * D + seg * kSeg;
-        const int ns = p.n_splits;
-        float m = -INFINITY;
-        for (int k = 0; k < ns; ++k) m = fmaxf(m, Mg[(size_t)k * R]);
-        float l = 0.f;
-        f32x4 acc[kSeg / 4];
+    const float l = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+
+    // Phase 2: weighted sum of the partial outputs.
+    const int lane = tid / kD4, d4 = tid % kD4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const float* Ob = p.Opart + base * D + 4 * d4;
+    int k = lane;
+    for (; k + 3 * kLanes < ns; k += 4 * kLanes) {
+        const f32x4 o0 = *reinterpret_cast<const f32x4*>(Ob + (size_t)k * R * D);
+        const f32x4 o1 = *reinterpret_cast<const f32x4*>(Ob + (size_t)(k + kLanes) * R * D);
+        const f32x4 o2 = *reinterpret_cast<const f32x4*>(Ob + (size_t)(k + 2 * kLanes) * R * D);
+        const f32x4 o3 = *reinterpret_cast<const f32x4*>(Ob + (size_t)(k + 3 * kLanes) * R * D);
+        acc += s_w[k] * o0 + s_w[k + kLanes] * o1 + s_w[k + 2 * kLanes] * o2 +
+               s_w[k + 3 * kLanes] * o3;
+    }
+    for (; k < ns; k += kLanes) acc += s_w[k] * *reinterpret_cast<const f32x4*>(Ob + (size_t)k * R * D);
+    s_acc[lane][d4] = acc;
+    __syncthreads();
+    if (tid < kD4) {
+        f32x4 t = s_acc[0][tid];
 #pragma unroll
-        for (int j = 0; j < kSeg / 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < ns; ++k) {
-            const float w = exp2_hw((Mg[(size_t)k * R] - m) * kLog2e);
-            l += w * Lg[(size_t)k * R];
-            const float* ok = Og + (size_t)k * R * D;
-#pragma unroll
-            for (int j = 0; j < kSeg / 4; ++j) acc[j] += w * *reinterpret_cast<const f32x4*>(ok + 4 * j);
-        }
-        const float inv = 1.0f / l;
-        const size_t ri = (size_t)grp * R + mrow;
-        float* dst = p.O + ri * D + seg * kSeg;
-#pragma unroll
-        for (int j = 0; j < kSeg / 4; ++j) *reinterpret_cast<f32x4*>(dst + 4 * j) = acc[j] * inv;
-        if (seg == 0) {
-            if (p.Mi) p.Mi[ri] = m;
-            if (p.Li) p.Li[ri] = l;
+        for (int j = 1; j < kLanes; ++j) t += s_acc[j][tid];
+        *reinterpret_cast<f32x4*>(p.O + (size_t)row * D + 4 * tid) = t * (1.0f / l);
+        if (tid == 0) {
+            if (p.Mi) p.Mi[row] = m;
+            if (p.Li) p.Li[row] = l;
         }
     }
 }

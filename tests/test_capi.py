@@ -118,9 +118,12 @@ def test_plan_null_out(lib):
 # ---------------------------------------------------------------------------
 def test_plans_for_baseline_configs():
     p = kf.plan(1, 4096, 4096, 32, 8, 128)           # C3 prefill
-    assert p.path == "prefill" and p.rows_per_group == 4 * 4096 and p.grid_blocks == 8 * 128
+    rows_per_block = p.block_threads // 64 * 32      # 32 query rows per wave
+    assert p.path == "prefill" and p.rows_per_group == 4 * 4096
+    assert p.grid_blocks == 8 * (4 * 4096 // rows_per_block)
     p = kf.plan(1, 512, 512, 32, 8, 128)             # C1
-    assert p.path == "prefill" and p.grid_blocks == 8 * 16 and p.workspace_bytes == 0
+    assert p.path == "prefill" and p.grid_blocks == 8 * (4 * 512 // rows_per_block)
+    assert p.workspace_bytes == 0
     p = kf.plan(1, 1, 4096, 32, 8, 128)              # C2 decode
     assert p.path == "decode_split" and p.rows_per_group == 4
     p = kf.plan(1, 2048, 2048, 32, 1, 64)            # C4a MQA prefill
@@ -145,7 +148,8 @@ def test_decode_split_geometry_covers_kv(B, q, kv, H_q, H_kv, D):
         assert p.path == "decode" and p.workspace_bytes == 0
     else:
         parts = B * H_q * q * p.num_splits
-        assert p.workspace_bytes >= parts * (D + 2) * 4 + B * H_kv * 8
+        assert p.workspace_bytes >= parts * (D + 2) * 4
+        assert p.num_splits <= 1024
 
 
 def test_prefill_threshold():
