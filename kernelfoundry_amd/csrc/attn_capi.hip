@@ -35,6 +35,7 @@ struct Plan {
     int rows_total;
     int n_splits;
     int kv_per_split;
+    int row_tiles;
     int grid;
     int threads;
     size_t ws_bytes;
@@ -73,12 +74,14 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) 
         p.threads = kf::kDecodeThreads;
         p.path = splits > 1 ? KF_PATH_DECODE_SPLIT : KF_PATH_DECODE;
     } else {
-        const long long row_tiles = (R + kf::kPrefillRows - 1) / kf::kPrefillRows;
+        const int rows = kf::prefill_rows_per_block(D);
+        const long long row_tiles = (R + rows - 1) / rows;
         if (n_groups * row_tiles > INT_MAX) return KF_ERR_SIZE;
         p.n_splits = 1;
         p.kv_per_split = kv_len;
+        p.row_tiles = (int)row_tiles;
         p.grid = (int)(n_groups * row_tiles);
-        p.threads = kf::kPrefillThreads;
+        p.threads = kf::prefill_threads(D);
         p.path = KF_PATH_PREFILL;
     }
     if (p.path == KF_PATH_DECODE_SPLIT) {
@@ -165,7 +168,7 @@ int kf_attn_fwd(const void* Q, const void* K, const void* V, float* O, float* ro
     }
     prm.rows_per_group = pl.R;
     prm.kv_len = kv_len;
-    prm.row_tiles = (pl.R + kf::kPrefillRows - 1) / kf::kPrefillRows;
+    prm.row_tiles = pl.row_tiles;
     prm.n_splits = pl.n_splits;
     prm.kv_per_split = pl.kv_per_split;
     prm.rows_total = pl.rows_total;

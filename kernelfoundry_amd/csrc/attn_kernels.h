@@ -361,27 +361,38 @@ template <> struct SwizzleRow<128> {
 };
 template <> struct SwizzleRow<256> : SwizzleRow<128> {};
 
-template <int D> struct PrefillCfg;
-template <> struct PrefillCfg<16>  { static constexpr int BC = 64;  static constexpr int kWavesPerEU = 2; };
-template <> struct PrefillCfg<64>  { static constexpr int BC = 128; static constexpr int kWavesPerEU = 2; };
-template <> struct PrefillCfg<128> { static constexpr int BC = 64;  static constexpr int kWavesPerEU = 2; };
-template <> struct PrefillCfg<256> { static constexpr int BC = 32;  static constexpr int kWavesPerEU = 1; };
+// Per head dimension: waves per workgroup (32 query rows each) and whether
+// S(t+1) = K Q^T is overlapped with the softmax of tile t (that needs a second
+// score block in registers).  D = 256 holds 128 fp32 O accumulators per lane,
+// so it runs 4 waves (one per SIMD, up to 512 registers) without the overlap.
+template <int D> struct PrefillCfg {
+    static constexpr int BC = 32;                   // KV rows per LDS stage
+    static constexpr int kWaves = D >= 256 ? 4 : 8;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kRows = 32 * kWaves;
+    static constexpr int kWavesPerEU = kWaves / 4;
+    static constexpr bool kPipeline = D <= 128;
+    // Pipelined: stages t, t+1 and the one being filled rotate through three
+    // LDS buffers; otherwise two suffice (and keep every LDS offset of D = 256
+    // inside the 16-bit instruction offset field).
+    static constexpr int kBuffers = kPipeline ? 3 : 2;
+};
 
-constexpr int kPrefillWaves = 8;                  // waves per workgroup, 32 query rows each
-constexpr int kPrefillThreads = 64 * kPrefillWaves;
-constexpr int kPrefillRows = 32 * kPrefillWaves;
+inline int prefill_rows_per_block(int D) { return D >= 256 ? PrefillCfg<256>::kRows : PrefillCfg<128>::kRows; }
+inline int prefill_threads(int D) { return D >= 256 ? PrefillCfg<256>::kThreads : PrefillCfg<128>::kThreads; }
 
-template <int D, int BC>
+template <int D, int BC, int NW>
 struct DmaStage {
     static constexpr int kRowBytes = D * 2;
     static constexpr int kChunks = D / 8;                        // 16-byte chunks per row
     static constexpr int kRowsPerInstr = 1024 / kRowBytes;       // rows per wave instruction
     static constexpr int kInstrPerTensor = BC * kRowBytes / 1024;
     static constexpr int kInstrTotal = 2 * kInstrPerTensor;      // K instructions, then V
-    static constexpr int kPerWave = (kInstrTotal + kPrefillWaves - 1) / kPrefillWaves;
+    static constexpr int kPerWave = (kInstrTotal + NW - 1) / NW;
     static constexpr int kTensorBytes = BC * kRowBytes;
     static constexpr int kStageBytes = 2 * kTensorBytes;         // K region, then V region
     static_assert(kRowsPerInstr * kRowBytes == 1024, "row size must divide 1 KiB");
+    static_assert(kInstrPerTensor >= 1, "a stage must fill whole KiB");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -394,18 +405,83 @@ __device__ __forceinline__ f16x4 lds_read_tr16(const char* lds_byte_ptr) {
     return __builtin_bit_cast(f16x4, v);
 }
 
+// Row max of NSB 32-row score blocks, shared with the partner lane l^32.
+template <int NSB>
+__device__ __forceinline__ float block_rowmax(const f32x16 (&s)[NSB]) {
+    float mx = fmaxf(s[0][0], s[0][1]);
+#pragma unroll
+    for (int b = 0; b < NSB; ++b)
+#pragma unroll
+        for (int r = (b == 0 ? 2 : 0); r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+    return fmaxf(mx, __shfl_xor(mx, 32));
+}
+
+template <int NSB>
+__device__ __forceinline__ void block_mask(f32x16 (&s)[NSB], int lim, int lane) {
+#pragma unroll
+    for (int b = 0; b < NSB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (32 * b + acc_row(r, lane) >= lim) s[b][r] = -INFINITY;
+}
+
+// exp2 + fp16 pack of one 32-row score block; returns its contribution to the
+// row sum (the fp16 P values, summed with v_dot2_f32_f16).
+__device__ __forceinline__ float block_exp(const f32x16& s, float scale_log2, float neg_m,
+                                           f16x8& p0, f16x8& p1) {
+    f32x8 e0, e1;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        e0[r] = exp2_hw(fmaf(s[r], scale_log2, neg_m));
+        e1[r] = exp2_hw(fmaf(s[8 + r], scale_log2, neg_m));
+    }
+    p0 = __builtin_convertvector(e0, f16x8);
+    p1 = __builtin_convertvector(e1, f16x8);
+    const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+    float a = 0.f, b = 0.f;
+    a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p0, p0, 0, 1), ones, a, false);
+    b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 0, 1), ones, b, false);
+    a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p0, p0, 2, 3), ones, a, false);
+    b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 2, 3), ones, b, false);
+    a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p0, p0, 4, 5), ones, a, false);
+    b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 4, 5), ones, b, false);
+    a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p0, p0, 6, 7), ones, a, false);
+    b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 6, 7), ones, b, false);
+    return a + b;
+}
+
+// Move the running max for a new block max (lazily) and rescale O and l.
+template <int NTD>
+__device__ __forceinline__ void block_update_max(RowState& st, float mx, float scale_log2,
+                                                 f32x16 (&o)[NTD]) {
+    st.rmax = fmaxf(st.rmax, mx);
+    const float mt = mx * scale_log2;
+    const bool need = mt > st.m + kLazyRescaleLog2;
+    if (__any(need)) {
+        const float mnew = need ? mt : st.m;
+        const float alpha = exp2_hw(st.m - mnew);
+        st.l *= alpha;
+#pragma unroll
+        for (int td = 0; td < NTD; ++td) o[td] *= alpha;
+        st.m = mnew;
+    }
+}
+
 template <int D>
-__global__ __launch_bounds__(kPrefillThreads, PrefillCfg<D>::kWavesPerEU)
+__global__ __launch_bounds__(PrefillCfg<D>::kThreads, PrefillCfg<D>::kWavesPerEU)
 void kf_attn_prefill_kernel(AttnParams p) {
     constexpr int BC = PrefillCfg<D>::BC;
-    using S = DmaStage<D, BC>;
-    using SW = SwizzleRow<D>;
     constexpr int kNSB = BC / 32;                 // 32-row score blocks per stage
+    constexpr int kPrefillWaves = PrefillCfg<D>::kWaves;
+    constexpr int kPrefillRows = PrefillCfg<D>::kRows;
+    using S = DmaStage<D, BC, kPrefillWaves>;
+    using SW = SwizzleRow<D>;
     constexpr int kNKK = D / 16;                  // MFMA k-steps over D
     constexpr int kNTD = (D < 32 ? 32 : D) / 32;  // 32-row O^T tiles
-    constexpr int kNJ = BC / 16;                  // P.V k-steps per stage
-    __shared__ __attribute__((aligned(1024))) char stage0[S::kStageBytes];
-    __shared__ __attribute__((aligned(1024))) char stage1[S::kStageBytes];
+    constexpr bool kPipe = PrefillCfg<D>::kPipeline;
+    __shared__ __attribute__((aligned(1024))) char buf0[S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char buf1[S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char buf2[kPipe ? S::kStageBytes : 16];
     __shared__ __attribute__((aligned(16))) char zero_pad[16];  // D=16: V^T rows 16..31
 
     const int tid = threadIdx.x;
@@ -418,6 +494,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const int R = p.rows_per_group;
     const int kv_len = p.kv_len;
     const int ntiles = (kv_len + BC - 1) / BC;
+    const float c = p.scale_log2;
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
     const char* Kh = reinterpret_cast<const char*>(p.K + (size_t)grp * kv_len * D);
@@ -481,7 +558,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     };
 
     // ---- Per-lane LDS read offsets (bytes within a stage). ----
-    // K (A of S^T = K Q^T): row l%32 (+32 sb), logical chunk 2 kk + g.
+    // K (A of S^T = K Q^T): row l%32, logical chunk 2 kk + g.
     int koff[kNKK];
 #pragma unroll
     for (int kk = 0; kk < kNKK; ++kk) {
@@ -501,17 +578,61 @@ void kf_attn_prefill_kernel(AttnParams p) {
                 const int r = 4 * (G >> 1) + (w >> 2) + 8 * h2;
                 const int d = 32 * td + 16 * (G & 1) + 4 * (w & 3);
                 if (d < D) {
-                    const int c = d >> 3, half = (d >> 2) & 1;
+                    const int cc = d >> 3, half = (d >> 2) & 1;
                     voff[td][h2] = S::kTensorBytes + r * S::kRowBytes +
-                                   ((c ^ SW::h(r)) % S::kChunks) * 16 + half * 8;
+                                   ((cc ^ SW::h(r)) % S::kChunks) * 16 + half * 8;
                 } else {
                     voff[td][h2] = -1;  // D=16 padding rows of V^T: read zeros
                 }
             }
     }
 
-    // ---- Prologue: stage 0 and the query fragments. ----
-    issue_stage(stage0, 0);
+    auto qk = [&](const char* stage, const f16x8 (&qf)[kNKK], f32x16 (&s)[kNSB]) {
+        // K fragments are fetched in batches of up to 8 (32 VGPRs).
+        constexpr int kBatch = kNKK < 8 ? kNKK : (D >= 256 ? 4 : 8);
+#pragma unroll
+        for (int b = 0; b < kNSB; ++b) {
+            s[b] = f32x16{};
+#pragma unroll
+            for (int k0 = 0; k0 < kNKK; k0 += kBatch) {
+                f16x8 kf[kBatch];
+#pragma unroll
+                for (int kk = 0; kk < kBatch; ++kk)
+                    kf[kk] = *reinterpret_cast<const f16x8*>(stage + koff[k0 + kk] +
+                                                             b * 32 * S::kRowBytes);
+#pragma unroll
+                for (int kk = 0; kk < kBatch; ++kk) s[b] = mfma32(kf[kk], qf[k0 + kk], s[b]);
+            }
+        }
+    };
+    // p[j] holds P^T for kv rows 16 j .. 16 j + 15 of the stage.
+    auto pv = [&](const char* stage, const f16x8 (&pp)[2 * kNSB], f32x16 (&o)[kNTD]) {
+#pragma unroll
+        for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+            for (int jj = 0; jj < 2 * kNSB; ++jj) {
+                f16x4 lo, hi;
+                if (D < 32 && voff[td][0] < 0) {
+                    lo = lds_read_tr16(zero_pad);
+                    hi = lo;
+                } else {
+                    lo = lds_read_tr16(stage + voff[td][0] + jj * 16 * S::kRowBytes);
+                    hi = lds_read_tr16(stage + voff[td][1] + jj * 16 * S::kRowBytes);
+                }
+                const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                o[td] = mfma32(a, pp[jj], o[td]);
+            }
+    };
+    auto softmax_exp = [&](const f32x16 (&s)[kNSB], float neg_m, f16x8 (&pp)[2 * kNSB]) {
+        float sum = 0.f;
+#pragma unroll
+        for (int b = 0; b < kNSB; ++b) sum += block_exp(s[b], c, neg_m, pp[2 * b], pp[2 * b + 1]);
+        return sum;
+    };
+
+    // ---- Prologue: stage 0 (and 1 when pipelined) in flight, Q fragments, S(0). ----
+    issue_stage(buf0, 0);
+    if (kPipe && ntiles > 1) issue_stage(buf1, BC);
     const int row = rt * kPrefillRows + wave * 32 + (lane & 31);
     f16x8 qf[kNKK];
     load_q_frags<D>(Qg, row, R, lane, qf);
@@ -525,56 +646,68 @@ void kf_attn_prefill_kernel(AttnParams p) {
     f32x16 o[kNTD];
 #pragma unroll
     for (int td = 0; td < kNTD; ++td) o[td] = f32x16{};
+    f32x16 sc[kNSB];
+    qk(buf0, qf, sc);
+    if (BC > kv_len) block_mask<kNSB>(sc, kv_len, lane);
+    block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, o);
 
-    auto compute_stage = [&](const char* cur, int t) {
-        f32x16 s[kNSB];
-#pragma unroll
-        for (int sb = 0; sb < kNSB; ++sb) {
-            f16x8 kf[kNKK];
-#pragma unroll
-            for (int kk = 0; kk < kNKK; ++kk)
-                kf[kk] = *reinterpret_cast<const f16x8*>(cur + koff[kk] + sb * 32 * S::kRowBytes);
-            s[sb] = f32x16{};
-#pragma unroll
-            for (int kk = 0; kk < kNKK; ++kk) s[sb] = mfma32(kf[kk], qf[kk], s[sb]);
-        }
-        if ((t + 1) * BC > kv_len) {
-            const int lim = kv_len - t * BC;
-#pragma unroll
-            for (int sb = 0; sb < kNSB; ++sb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (32 * sb + acc_row(r, lane) >= lim) s[sb][r] = -INFINITY;
-        }
-        f16x8 pb[kNJ];
-        softmax_update<kNSB, kNTD>(s, st, o, p.scale_log2, pb);
-#pragma unroll
-        for (int td = 0; td < kNTD; ++td)
-#pragma unroll
-            for (int jj = 0; jj < kNJ; ++jj) {
-                f16x4 lo, hi;
-                if (D < 32 && voff[td][0] < 0) {
-                    lo = lds_read_tr16(zero_pad);
-                    hi = lo;
-                } else {
-                    lo = lds_read_tr16(cur + voff[td][0] + jj * 16 * S::kRowBytes);
-                    hi = lds_read_tr16(cur + voff[td][1] + jj * 16 * S::kRowBytes);
-                }
-                const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                o[td] = mfma32(a, pb[jj], o[td]);
+    // ---- One pipelined tile; S(t) and its running max are ready on entry.
+    //   barrier; LDS-DMA of stage t+2
+    //   S(t+1) = K(t+1) Q^T   | exp + fp16 pack of S(t)
+    //   O += V(t) P(t)        | row max of S(t+1)
+    //   rare: tail masking of S(t+1); lazy rescale of O
+    // Stages rotate through three LDS buffers.  On the last tile the S(t+1)
+    // MFMAs read a stale, in-bounds buffer and are discarded, which keeps the
+    // overlapped regions free of branches (issue is in order: a wave can only
+    // overlap MFMA and VALU work that is interleaved in its own stream).
+    auto tile = [&](const char* cur, const char* nxt, char* fill, int t) {
+        f16x8 pp[2 * kNSB];
+        if constexpr (!kPipe) {
+            // Two buffers: stage t+1 loads into `nxt` while stage t is used.
+            if (t + 1 < ntiles) issue_stage(const_cast<char*>(nxt), (t + 1) * BC);
+            if (t > 0) {
+                qk(cur, qf, sc);
+                if ((t + 1) * BC > kv_len) block_mask<kNSB>(sc, kv_len - t * BC, lane);
+                block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, o);
             }
+            st.l += softmax_exp(sc, -st.m, pp);
+            pv(cur, pp, o);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();  // stage t+1 landed; every wave is done with stage t
+            return;
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // stage t+1 landed for every wave; stage t-1 is free
+        if (t + 2 < ntiles) issue_stage(fill, (t + 2) * BC);
+        f32x16 sn[kNSB];
+        qk(nxt, qf, sn);
+        st.l += softmax_exp(sc, -st.m, pp);
+        pv(cur, pp, o);
+        float mx = block_rowmax<kNSB>(sn);
+        if (t + 1 < ntiles) {
+            if ((t + 2) * BC > kv_len) {  // S(t+1) is the partial last tile
+                block_mask<kNSB>(sn, kv_len - (t + 1) * BC, lane);
+                mx = block_rowmax<kNSB>(sn);
+            }
+            block_update_max<kNTD>(st, mx, c, o);
+#pragma unroll
+            for (int b = 0; b < kNSB; ++b) sc[b] = sn[b];
+        }
     };
-
-    for (int t = 0; t < ntiles; t += 2) {
-        if (t + 1 < ntiles) issue_stage(stage1, (t + 1) * BC);
-        compute_stage(stage0, t);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (t + 1 >= ntiles) break;
-        if (t + 2 < ntiles) issue_stage(stage0, (t + 2) * BC);
-        compute_stage(stage1, t + 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+    if constexpr (kPipe) {
+        for (int t = 0; t < ntiles; t += 3) {
+            tile(buf0, buf1, buf2, t);
+            if (t + 1 >= ntiles) break;
+            tile(buf1, buf2, buf0, t + 1);
+            if (t + 2 >= ntiles) break;
+            tile(buf2, buf0, buf1, t + 2);
+        }
+    } else {
+        for (int t = 0; t < ntiles; t += 2) {
+            tile(buf0, buf1, nullptr, t);
+            if (t + 1 >= ntiles) break;
+            tile(buf1, buf0, nullptr, t + 1);
+        }
     }
 
     // ---- Epilogue: combine the two half-row partial sums, normalise, store. ----
