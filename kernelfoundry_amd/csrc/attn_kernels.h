@@ -3,9 +3,10 @@
 // Three kernels, all hand-written for wave64 and the fp16 MFMA
 // v_mfma_f32_32x32x16_f16:
 //
-//   kf_attn_prefill_kernel<D>  one workgroup = 4 waves = 128 query rows of one
-//                              KV head; K/V streamed through double-buffered
-//                              LDS stages; online softmax in registers.
+//   kf_attn_prefill_kernel<D>  one workgroup = 8 waves (4 for D = 256) x 32
+//                              query rows of one KV head; K/V streamed
+//                              HBM -> LDS by LDS-DMA through a ring of LDS
+//                              stages; online softmax in registers.
 //   kf_attn_decode_kernel<D>   split-KV ("flash-decoding") for <= 32 query
 //                              rows per KV head (Q_len = 1 decode, GQA/MQA
 //                              groups): every wave streams its own KV stages
@@ -329,15 +330,15 @@ __device__ __forceinline__ void pv_accum(const f16* __restrict__ Vt, int kv0,
 }
 
 // ---------------------------------------------------------------------------
-// Prefill: 4 waves x 32 query rows per workgroup.  K and V stages of BC rows
-// are copied HBM -> LDS by the gfx950 LDS-DMA loads (global_load_lds_dwordx4:
-// each wave instruction fills one contiguous KiB of LDS, no VGPR staging),
-// double-buffered in two named LDS arrays so the prefetch of stage t+1
-// overlaps the MFMA/softmax work on stage t.  Both K and V stay row-major in
-// LDS with the 16-byte chunks of a row XOR-permuted by SwizzleRow<D>: K
-// fragments are read with ds_read_b128, and the V^T fragments of the P.V
-// MFMA with the transposing ds_read_b64_tr_b16, so V is never transposed by
-// VALU work.
+// Prefill: 8 waves (D = 256: 4) x 32 query rows per workgroup.  K and V
+// stages are copied HBM -> LDS by the gfx950 LDS-DMA loads
+// (global_load_lds_dwordx4: each wave instruction fills one contiguous KiB
+// of LDS, no VGPR staging) into named LDS arrays, so the prefetch of later
+// stages overlaps the MFMA/softmax work on the current one.  Both K and V
+// stay row-major in LDS with the 16-byte chunks of a row XOR-permuted by
+// SwizzleRow<D>: K fragments are read with ds_read_b128, and the V^T
+// fragments of the P.V MFMA with the transposing ds_read_b64_tr_b16, so V is
+// never transposed by VALU work.
 // ---------------------------------------------------------------------------
 
 // Row-dependent XOR applied to the 16-byte chunk index of a K / V row in LDS.
@@ -366,7 +367,7 @@ template <> struct SwizzleRow<256> : SwizzleRow<128> {};
 // score block in registers).  D = 256 holds 128 fp32 O accumulators per lane,
 // so it runs 4 waves (one per SIMD, up to 512 registers) without the overlap.
 template <int D> struct PrefillCfg {
-    static constexpr int BC = 32;                   // KV rows per LDS stage
+    static constexpr int BC = 32;                   // KV rows per MFMA tile
     static constexpr int kWaves = D >= 256 ? 4 : 8;
     static constexpr int kThreads = 64 * kWaves;
     static constexpr int kRows = 32 * kWaves;
@@ -376,6 +377,10 @@ template <int D> struct PrefillCfg {
     // LDS buffers; otherwise two suffice (and keep every LDS offset of D = 256
     // inside the 16-bit instruction offset field).
     static constexpr int kBuffers = kPipeline ? 3 : 2;
+    // Tiles per LDS stage.  Pipelined, one stage holds two tiles, so the
+    // workgroup barrier and the LDS-DMA issue come once per 64 kv rows.
+    static constexpr int kSub = kPipeline ? 2 : 1;
+    static constexpr int kStageRows = BC * kSub;
 };
 
 inline int prefill_rows_per_block(int D) { return D >= 256 ? PrefillCfg<256>::kRows : PrefillCfg<128>::kRows; }
@@ -474,7 +479,8 @@ void kf_attn_prefill_kernel(AttnParams p) {
     constexpr int kNSB = BC / 32;                 // 32-row score blocks per stage
     constexpr int kPrefillWaves = PrefillCfg<D>::kWaves;
     constexpr int kPrefillRows = PrefillCfg<D>::kRows;
-    using S = DmaStage<D, BC, kPrefillWaves>;
+    constexpr int SR = PrefillCfg<D>::kStageRows;  // kv rows per LDS stage
+    using S = DmaStage<D, SR, kPrefillWaves>;
     using SW = SwizzleRow<D>;
     constexpr int kNKK = D / 16;                  // MFMA k-steps over D
     constexpr int kNTD = (D < 32 ? 32 : D) / 32;  // 32-row O^T tiles
@@ -493,7 +499,8 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const int grp = blk / p.row_tiles;
     const int R = p.rows_per_group;
     const int kv_len = p.kv_len;
-    const int ntiles = (kv_len + BC - 1) / BC;
+    const int ntiles = (kv_len + BC - 1) / BC;    // 32-row tiles
+    const int nstages = (kv_len + SR - 1) / SR;   // LDS stages
     const float c = p.scale_log2;
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
@@ -517,7 +524,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
                                   (((lane % S::kChunks) ^ SW::h(r)) % S::kChunks) * 16);
     }
     auto issue_stage = [&](char* dst, int kv0) {
-        if (kv0 + BC <= kv_len) {
+        if (kv0 + SR <= kv_len) {
             // Full stage: wave-uniform row base (SGPRs) + the lane's constant
             // 32-bit offset; no per-lane address arithmetic.
 #pragma unroll
@@ -632,7 +639,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
 
     // ---- Prologue: stage 0 (and 1 when pipelined) in flight, Q fragments, S(0). ----
     issue_stage(buf0, 0);
-    if (kPipe && ntiles > 1) issue_stage(buf1, BC);
+    if (kPipe && nstages > 1) issue_stage(buf1, SR);
     const int row = rt * kPrefillRows + wave * 32 + (lane & 31);
     f16x8 qf[kNKK];
     load_q_frags<D>(Qg, row, R, lane, qf);
@@ -660,7 +667,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     // MFMAs read a stale, in-bounds buffer and are discarded, which keeps the
     // overlapped regions free of branches (issue is in order: a wave can only
     // overlap MFMA and VALU work that is interleaved in its own stream).
-    auto tile = [&](const char* cur, const char* nxt, char* fill, int t) {
+    auto tile = [&](const char* cur, const char* nxt, char* fill, int t, bool sync) {
         f16x8 pp[2 * kNSB];
         if constexpr (!kPipe) {
             // Two buffers: stage t+1 loads into `nxt` while stage t is used.
@@ -676,9 +683,15 @@ void kf_attn_prefill_kernel(AttnParams p) {
             __syncthreads();  // stage t+1 landed; every wave is done with stage t
             return;
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();  // stage t+1 landed for every wave; stage t-1 is free
-        if (t + 2 < ntiles) issue_stage(fill, (t + 2) * BC);
+        if (sync) {
+            // Tile t is the second of its stage j = t / 2, tile t+1 the first
+            // of stage j+1: wait until stage j+1 landed for every wave; stage
+            // j-1 (last read by tile t-1) is then free for stage j+2.
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            const int js = (t >> 1) + 2;
+            if (js < nstages) issue_stage(fill, js * SR);
+        }
         f32x16 sn[kNSB];
         qk(nxt, qf, sn);
         st.l += softmax_exp(sc, -st.m, pp);
@@ -686,6 +699,9 @@ void kf_attn_prefill_kernel(AttnParams p) {
         float mx = block_rowmax<kNSB>(sn);
         if (t + 1 < ntiles) {
             if ((t + 2) * BC > kv_len) {  // S(t+1) is the partial last tile
+                // Keep this a branch: if-converted, the compares and selects
+                // of the mask would run on every tile.
+                asm volatile("" ::: "memory");
                 block_mask<kNSB>(sn, kv_len - (t + 1) * BC, lane);
                 mx = block_rowmax<kNSB>(sn);
             }
@@ -695,18 +711,27 @@ void kf_attn_prefill_kernel(AttnParams p) {
         }
     };
     if constexpr (kPipe) {
-        for (int t = 0; t < ntiles; t += 3) {
-            tile(buf0, buf1, buf2, t);
+        // Tile t reads the (t % 2)-th half of stage t / 2, which lives in
+        // buffer (t / 2) % 3; the loop body covers 3 stages.
+        constexpr int H = BC * S::kRowBytes;
+        for (int t = 0; t < ntiles; t += 6) {
+            tile(buf0, buf0 + H, nullptr, t, false);
             if (t + 1 >= ntiles) break;
-            tile(buf1, buf2, buf0, t + 1);
+            tile(buf0 + H, buf1, buf2, t + 1, true);
             if (t + 2 >= ntiles) break;
-            tile(buf2, buf0, buf1, t + 2);
+            tile(buf1, buf1 + H, nullptr, t + 2, false);
+            if (t + 3 >= ntiles) break;
+            tile(buf1 + H, buf2, buf0, t + 3, true);
+            if (t + 4 >= ntiles) break;
+            tile(buf2, buf2 + H, nullptr, t + 4, false);
+            if (t + 5 >= ntiles) break;
+            tile(buf2 + H, buf0, buf1, t + 5, true);
         }
     } else {
         for (int t = 0; t < ntiles; t += 2) {
-            tile(buf0, buf1, nullptr, t);
+            tile(buf0, buf1, nullptr, t, false);
             if (t + 1 >= ntiles) break;
-            tile(buf1, buf0, nullptr, t + 1);
+            tile(buf1, buf0, nullptr, t + 1, false);
         }
     }
 
