@@ -479,6 +479,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     constexpr int kNSB = BC / 32;                 // 32-row score blocks per stage
     constexpr int kPrefillWaves = PrefillCfg<D>::kWaves;
     constexpr int kPrefillRows = PrefillCfg<D>::kRows;
+    constexpr int kSub = PrefillCfg<D>::kSub;      // tiles per LDS stage
     constexpr int SR = PrefillCfg<D>::kStageRows;  // kv rows per LDS stage
     using S = DmaStage<D, SR, kPrefillWaves>;
     using SW = SwizzleRow<D>;
@@ -684,12 +685,12 @@ void kf_attn_prefill_kernel(AttnParams p) {
             return;
         }
         if (sync) {
-            // Tile t is the second of its stage j = t / 2, tile t+1 the first
+            // Tile t is the last of its stage j = t / kSub, tile t+1 the first
             // of stage j+1: wait until stage j+1 landed for every wave; stage
             // j-1 (last read by tile t-1) is then free for stage j+2.
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-            const int js = (t >> 1) + 2;
+            const int js = t / kSub + 2;
             if (js < nstages) issue_stage(fill, js * SR);
         }
         f32x16 sn[kNSB];
@@ -710,7 +711,16 @@ void kf_attn_prefill_kernel(AttnParams p) {
             for (int b = 0; b < kNSB; ++b) sc[b] = sn[b];
         }
     };
-    if constexpr (kPipe) {
+    if constexpr (kPipe && kSub == 1) {
+        for (int t = 0; t < ntiles; t += 3) {
+            tile(buf0, buf1, buf2, t, true);
+            if (t + 1 >= ntiles) break;
+            tile(buf1, buf2, buf0, t + 1, true);
+            if (t + 2 >= ntiles) break;
+            tile(buf2, buf0, buf1, t + 2, true);
+        }
+    } else if constexpr (kPipe) {
+        static_assert(kSub == 2, "pipelined stages hold one or two tiles");
         // Tile t reads the (t % 2)-th half of stage t / 2, which lives in
         // buffer (t / 2) % 3; the loop body covers 3 stages.
         constexpr int H = BC * S::kRowBytes;
