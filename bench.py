@@ -15,6 +15,9 @@ half of the metric):
                      the figure is an HBM figure, not a cache figure.
   * ``decode_b32`` -- configs[4]: B=32, KV=8192 (1.07 GB of unique K/V per
                      step), the clean HBM-streaming case.
+  * ``prefill_causal`` -- the configs[2] shape with the causal mask of
+                     kf_attn_fwd_ex; FLOPs count only the visible pairs,
+                     4*B*H_q*D*S(S+1)/2.
   * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep)
                      and the MQA D=64 configs[3].
 
@@ -52,6 +55,12 @@ def flops(B, H_q, q, kv, D):
     return 4.0 * B * H_q * q * kv * D
 
 
+def causal_flops(B, H_q, S, D):
+    """Algorithmic FLOPs of causal attention with q_len = kv_len = S: query i
+    sees i + 1 keys, so sum_i (i + 1) = S (S + 1) / 2 score/PV pairs."""
+    return 4.0 * B * H_q * D * S * (S + 1) / 2
+
+
 def nbytes(B, H_q, H_kv, q, kv, D):
     qn, kvn = B * H_q * q * D, B * H_kv * kv * D
     return 2.0 * qn + 4.0 * kvn + 4.0 * qn
@@ -69,8 +78,9 @@ def _inputs(torch, B, H_q, H_kv, q, kv, D, seed):
 class Runner:
     """Pre-resolved kf_attn_fwd call (no allocation inside the timed loop)."""
 
-    def __init__(self, torch, kf, sets, D):
+    def __init__(self, torch, kf, sets, D, flags=0):
         self.torch, self.kf = torch, kf
+        self.flags = flags
         Q, K, V = sets[0]
         B, H_q, q, _ = Q.shape
         _, H_kv, kv, _ = K.shape
@@ -89,10 +99,17 @@ class Runner:
         self.i += 1
         Q, K, V = self.sets[j]
         B, q, kv, H_q, H_kv, D = self.shape
-        st = self.lib.kf_attn_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(), self.outs[j].data_ptr(),
-                                  None, None, B, q, kv, H_q, H_kv, D,
-                                  self.ws.data_ptr() if self.ws_bytes else None, self.ws_bytes,
-                                  self.stream.cuda_stream)
+        if self.flags:
+            st = self.lib.kf_attn_fwd_ex(Q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                                         self.outs[j].data_ptr(), None, None, B, q, kv, H_q, H_kv,
+                                         D, None, self.flags,
+                                         self.ws.data_ptr() if self.ws_bytes else None,
+                                         self.ws_bytes, self.stream.cuda_stream)
+        else:
+            st = self.lib.kf_attn_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                                      self.outs[j].data_ptr(), None, None, B, q, kv, H_q, H_kv, D,
+                                      self.ws.data_ptr() if self.ws_bytes else None,
+                                      self.ws_bytes, self.stream.cuda_stream)
         if st != 0:
             raise RuntimeError(f"kf_attn_fwd failed: {self.kf.status_string(st)}")
         return j
@@ -125,7 +142,7 @@ def time_steps(torch, runner, steps, warmup):
     return ms_step, statistics.mean(per), statistics.median(per)
 
 
-def parity_spot_check(torch, runner, heads):
+def parity_spot_check(torch, runner, heads, causal=False):
     """Compare the last outputs on a few heads with the fp64 oracle."""
     from oracle import attn_oracle as orc
     import numpy as np
@@ -137,7 +154,8 @@ def parity_spot_check(torch, runner, heads):
     worst = (0.0, 0.0)
     for b, h in heads:
         hk = h // (H_q // H_kv)
-        ref, _, _ = orc.sdpa(Q[b:b + 1, h:h + 1], K[b:b + 1, hk:hk + 1], V[b:b + 1, hk:hk + 1])
+        ref, _, _ = orc.sdpa(Q[b:b + 1, h:h + 1], K[b:b + 1, hk:hk + 1], V[b:b + 1, hk:hk + 1],
+                             causal=causal)
         ok, mx, rel = orc.within_tolerance(O[b:b + 1, h:h + 1], ref)
         if not ok:
             raise AssertionError(f"bench parity failed on head ({b},{h}): max_abs={mx} rel={rel}")
@@ -203,7 +221,8 @@ def main():
     ap.add_argument("--decode-sets", type=int, default=40,
                     help="distinct Q/K/V sets rotated through for the KV=4096 decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "decode_b32", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "prefill_causal", "decode", "decode_b32", "copy"],
+                    default=None,
                     help="run one workload only (for rocprof counter passes); prints no JSON")
     args = ap.parse_args()
 
@@ -254,6 +273,24 @@ def main():
         results["prefill"] = run_prefill(4096, check=[(0, 0), (0, 31)] if args.only is None else None)
         if args.only:
             return
+
+    if args.only in (None, "prefill_causal"):
+        print("bench: causal prefill S=4096 GQA D=128", file=sys.stderr, flush=True)
+        sets = [_inputs(torch, 1, 32, 8, 4096, 4096, 128, 1234 + 4096)]
+        rc = Runner(torch, kf, sets, 128, flags=kf.KF_ATTN_CAUSAL)
+        ms, kern_mean, _ = time_steps(torch, rc, steps, warmup)
+        if args.only:
+            return
+        f = causal_flops(1, 32, 4096, 128)
+        results["prefill_causal"] = {
+            "config": "configs[2] shape, causal (kf_attn_fwd_ex, bottom-right aligned)",
+            "ms": round(ms, 5), "tflops": round(f / (ms * 1e9), 2),
+            "kernel_ms_mean": round(kern_mean, 5), "kernel_tflops": round(f / (kern_mean * 1e9), 2),
+            "algorithmic_flops_per_launch": f,
+            "frac": round(f / (kern_mean * 1e9) / PEAK_FP16_TFLOPS, 4),
+            "parity": parity_spot_check(torch, rc, [(0, 0), (0, 31)], causal=True),
+        }
+        del rc
 
     def run_decode(B, kv, n_sets, D=128, H_kv=8):
         sets = [_inputs(torch, B, 32, H_kv, 1, kv, D, 99 + i) for i in range(n_sets)]
@@ -345,6 +382,7 @@ def main():
             "path": b32["path"], "splits": b32["splits"],
             "parity": b32["parity"],
         },
+        "prefill_causal": results["prefill_causal"],
         "sweep": sweep,
         "parity": pre.get("parity"),
     }

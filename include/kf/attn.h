@@ -23,8 +23,11 @@
  *   Li [B, H_q,  q_len]      fp32, optional: sum_j exp(s_ij - Mi)
  * Query head h_q reads KV head h_q / (H_q / H_kv) (flash_attn.cu:406); H_q
  * must be a multiple of H_kv (the reference silently mis-groups otherwise).
- * Attention is non-causal and the softmax scale is 1/sqrt(D), as in the
- * reference.  D must be one of the reference's instantiations
+ * kf_attn_fwd is non-causal with softmax scale 1/sqrt(D), as in the
+ * reference; kf_attn_fwd_ex adds causal masking and per-sequence key
+ * counts (ranked next steps of the reference's own roadmap,
+ * docs/flash_attn.md:105 and tests/bench_flash_attn2.py:115-150).
+ * D must be one of the reference's instantiations
  * {16, 64, 128, 256} (flash_attn.cu:587-600).  All device pointers must be
  * 16-byte aligned.
  */
@@ -47,8 +50,12 @@ enum kf_status {
     KF_ERR_NULL = 4,       /* a required pointer is NULL                        */
     KF_ERR_WORKSPACE = 5,  /* workspace missing or smaller than required        */
     KF_ERR_ALIGN = 6,      /* a device pointer is not 16-byte aligned           */
-    KF_ERR_HIP = 7         /* a HIP runtime call failed: kf_last_hip_error()    */
+    KF_ERR_HIP = 7,        /* a HIP runtime call failed: kf_last_hip_error()    */
+    KF_ERR_FLAGS = 8       /* kf_attn_fwd_ex: unknown bits in `flags`            */
 };
+
+/* kf_attn_fwd_ex flags. */
+#define KF_ATTN_CAUSAL 1   /* query i sees keys j <= i + kv_b - q_len           */
 
 /* Which kernels kf_attn_fwd runs for a shape (see kf_attn_plan). */
 enum kf_path {
@@ -94,6 +101,28 @@ int kf_attn_fwd(const void* Q, const void* K, const void* V, float* O,
                 float* row_max, float* row_sumexp,
                 int B, int q_len, int kv_len, int H_q, int H_kv, int D,
                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* kf_attn_fwd with key masking; kf_attn_fwd(...) == kf_attn_fwd_ex(...,
+ * NULL, 0, ...).  No counterpart in the reference, which has neither
+ * (flash_attn.cu:384-585 is non-causal over all kv_len keys).
+ *
+ * kv_lens: NULL, or a device array [B] of int (4-byte aligned): sequence b
+ *   uses only its first kv_b = kv_lens[b] keys (clamped to [0, kv_len]) of
+ *   the kv_len rows allocated per head in K / V -- a pre-allocated KV cache
+ *   filled to different lengths.
+ * flags & KF_ATTN_CAUSAL: query i (0 <= i < q_len) of sequence b sees keys
+ *   j <= i + kv_b - q_len, i.e. the mask is aligned to the bottom-right
+ *   corner (the last query sees every key; with q_len == kv_len it is the
+ *   usual lower triangle; q_len = 1 decode is unaffected).
+ * A query row that sees no key (kv_b = 0, or causal rows with
+ * i + kv_b - q_len < 0) gets O = 0, Mi = -inf, Li = 0.  Shapes, workspace
+ * and the kernels chosen are those of kf_attn_fwd (kf_attn_plan,
+ * kf_attn_workspace_bytes apply unchanged). */
+int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, float* O,
+                   float* row_max, float* row_sumexp,
+                   int B, int q_len, int kv_len, int H_q, int H_kv, int D,
+                   const int* kv_lens, int flags,
+                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* The reference launcher's contract (tests/test_flash_attn.cu:52-113):
  * q_len = kv_len = S, scratch allocated and freed by the call, stream

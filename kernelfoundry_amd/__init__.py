@@ -15,6 +15,9 @@ Interface, mirroring the reference harness (sviraaj/kernelfoundry):
   separate q_len / kv_len (decode) and optional Mi / Li outputs, as the
   bench's ``launch_once`` (tests/bench_flash_attn.cu:39-54).
 * ``attn_fwd_ptr(...)`` -- the same on raw pointers, returning the kf status.
+* ``attn_fwd(..., causal=True, kv_lens=...)`` / ``attn_fwd_ex_ptr(...)`` --
+  kf_attn_fwd_ex: bottom-right-aligned causal masking and per-sequence key
+  counts over a pre-allocated K/V cache (no reference counterpart).
 * ``plan(B, q_len, kv_len, H_q, H_kv, D)`` -- which kernels run, GPU-free.
 """
 from __future__ import annotations
@@ -28,7 +31,8 @@ __all__ = [
     "KfError", "LIB_PATH", "load_library", "plan", "workspace_bytes", "attn_fwd",
     "attn_fwd_ptr", "launch_flash_attn", "status_string", "exported_symbols",
     "KF_OK", "KF_ERR_HEAD_DIM", "KF_ERR_GQA", "KF_ERR_SIZE", "KF_ERR_NULL",
-    "KF_ERR_WORKSPACE", "KF_ERR_ALIGN", "KF_ERR_HIP", "PATH_NAMES",
+    "KF_ERR_WORKSPACE", "KF_ERR_ALIGN", "KF_ERR_HIP", "KF_ERR_FLAGS", "KF_ATTN_CAUSAL",
+    "PATH_NAMES", "attn_fwd_ex_ptr",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -43,6 +47,8 @@ KF_ERR_NULL = 4
 KF_ERR_WORKSPACE = 5
 KF_ERR_ALIGN = 6
 KF_ERR_HIP = 7
+KF_ERR_FLAGS = 8
+KF_ATTN_CAUSAL = 1
 
 PATH_NAMES = {0: "prefill", 1: "decode", 2: "decode_split"}
 
@@ -99,6 +105,8 @@ def load_library(path: str = LIB_PATH):
     lib.kf_attn_workspace_bytes.restype = sz
     lib.kf_attn_fwd.argtypes = [p, p, p, p, p, p] + [i] * 6 + [p, sz, p]
     lib.kf_attn_fwd.restype = i
+    lib.kf_attn_fwd_ex.argtypes = [p, p, p, p, p, p] + [i] * 6 + [p, i, p, sz, p]
+    lib.kf_attn_fwd_ex.restype = i
     lib.kf_launch_flash_attn.argtypes = [p, p, p, p] + [i] * 5 + [p]
     lib.kf_launch_flash_attn.restype = i
     lib.kf_status_string.argtypes = [i]
@@ -142,17 +150,27 @@ def attn_fwd_ptr(Q, K, V, O, Mi, Li, B, q_len, kv_len, H_q, H_kv, D, workspace=0
                                           stream or None))
 
 
+def attn_fwd_ex_ptr(Q, K, V, O, Mi, Li, B, q_len, kv_len, H_q, H_kv, D, kv_lens=0, flags=0,
+                    workspace=0, workspace_bytes=0, stream=0) -> int:
+    """kf_attn_fwd_ex on raw device addresses (ints); returns the kf status."""
+    return int(load_library().kf_attn_fwd_ex(Q, K, V, O, Mi or None, Li or None, B, q_len,
+                                             kv_len, H_q, H_kv, D, kv_lens or None, flags,
+                                             workspace or None, workspace_bytes, stream or None))
+
+
 def launch_flash_attn(Q, K, V, O, B, S, H_q, H_kv, D, stream=0) -> int:
     """Reference launcher contract on raw device addresses; returns hipError_t."""
     return int(load_library().kf_launch_flash_attn(Q, K, V, O, B, S, H_q, H_kv, D, stream or None))
 
 
-def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=None):
+def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=None,
+             causal=False, kv_lens=None):
     """Attention forward on torch tensors resident on the GPU.
 
     Q [B, H_q, q_len, D] fp16, K/V [B, H_kv, kv_len, D] fp16, contiguous.
     Returns O [B, H_q, q_len, D] fp32, or (O, Mi, Li) with ``return_stats``.
     Asynchronous on ``stream`` (default: torch's current stream).
+    ``causal`` / ``kv_lens`` (int32 GPU tensor [B]) select kf_attn_fwd_ex.
     """
     import torch
 
@@ -180,12 +198,18 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=Q.device)
         workspace.record_stream(stream)
-    st = attn_fwd_ptr(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(),
-                      Mi.data_ptr() if Mi is not None else 0,
-                      Li.data_ptr() if Li is not None else 0,
-                      B, q_len, kv_len, H_q, H_kv, D,
-                      workspace.data_ptr() if (need and workspace is not None) else 0,
-                      need, stream.cuda_stream)
+    if kv_lens is not None:
+        if kv_lens.dtype != torch.int32 or not kv_lens.is_cuda or kv_lens.numel() != B:
+            raise ValueError("kv_lens must be an int32 GPU tensor of B elements")
+        kv_lens = kv_lens.contiguous()
+    st = attn_fwd_ex_ptr(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(),
+                         Mi.data_ptr() if Mi is not None else 0,
+                         Li.data_ptr() if Li is not None else 0,
+                         B, q_len, kv_len, H_q, H_kv, D,
+                         kv_lens.data_ptr() if kv_lens is not None else 0,
+                         KF_ATTN_CAUSAL if causal else 0,
+                         workspace.data_ptr() if (need and workspace is not None) else 0,
+                         need, stream.cuda_stream)
     if st != KF_OK:
         msg = status_string(st)
         if st == KF_ERR_HIP:

@@ -105,7 +105,10 @@ int hip_fail(hipError_t e) {
 template <int D>
 hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t stream) {
     if (pl.path == KF_PATH_PREFILL) {
-        kf::kf_attn_prefill_kernel<D><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+        if (prm.causal || prm.kv_lens)
+            kf::kf_attn_prefill_kernel<D, true><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+        else
+            kf::kf_attn_prefill_kernel<D, false><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
         return hipGetLastError();
     }
     kf::kf_attn_decode_kernel<D><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
@@ -143,11 +146,21 @@ size_t kf_attn_workspace_bytes(int B, int q_len, int kv_len, int H_q, int H_kv, 
 int kf_attn_fwd(const void* Q, const void* K, const void* V, float* O, float* row_max,
                 float* row_sumexp, int B, int q_len, int kv_len, int H_q, int H_kv, int D,
                 void* workspace, size_t workspace_bytes, void* stream) {
+    return kf_attn_fwd_ex(Q, K, V, O, row_max, row_sumexp, B, q_len, kv_len, H_q, H_kv, D,
+                          nullptr, 0, workspace, workspace_bytes, stream);
+}
+
+int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, float* O, float* row_max,
+                   float* row_sumexp, int B, int q_len, int kv_len, int H_q, int H_kv, int D,
+                   const int* kv_lens, int flags, void* workspace, size_t workspace_bytes,
+                   void* stream) {
     Plan pl;
     const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, &pl);
     if (st != KF_OK) return st;
+    if ((flags & ~KF_ATTN_CAUSAL) != 0) return KF_ERR_FLAGS;
     if (!Q || !K || !V || !O) return KF_ERR_NULL;
     if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O)) return KF_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(kv_lens) & 3u) != 0) return KF_ERR_ALIGN;
     if (pl.ws_bytes > 0) {
         if (!workspace || workspace_bytes < pl.ws_bytes) return KF_ERR_WORKSPACE;
         if ((reinterpret_cast<uintptr_t>(workspace) & (kWsAlign - 1)) != 0) return KF_ERR_ALIGN;
@@ -175,6 +188,10 @@ int kf_attn_fwd(const void* Q, const void* K, const void* V, float* O, float* ro
     const double scale = 1.0 / __builtin_sqrt((double)D);
     prm.scale = 1.0f / __builtin_sqrtf((float)D);  // the reference's fp32 scale
     prm.scale_log2 = (float)(scale * 1.4426950408889634);
+    prm.kv_lens = kv_lens;
+    prm.causal = (flags & KF_ATTN_CAUSAL) ? 1 : 0;
+    prm.q_len = q_len;
+    prm.heads_kv = H_kv;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
@@ -226,6 +243,7 @@ const char* kf_status_string(int status) {
         case KF_ERR_WORKSPACE: return "workspace missing or smaller than kf_attn_workspace_bytes()";
         case KF_ERR_ALIGN: return "device pointer not 16-byte aligned (workspace: 256-byte)";
         case KF_ERR_HIP: return "HIP runtime error (see kf_last_hip_error)";
+        case KF_ERR_FLAGS: return "unknown flag bits (only KF_ATTN_CAUSAL is defined)";
         default: return "unknown status";
     }
 }

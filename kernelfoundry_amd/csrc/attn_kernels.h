@@ -86,7 +86,42 @@ struct AttnParams {
     int rows_total;     // B * H_q * q_len
     float scale;        // 1 / sqrt(D), fp32 (the reference's softmax scale)
     float scale_log2;   // scale * log2(e)
+    // Key masking (kf_attn_fwd_ex).  Sequence b uses keys [0, kv_lens[b])
+    // of its K/V rows (kv_len rows are allocated per head); with `causal`,
+    // query i of q_len additionally sees keys j <= i + kv_lens[b] - q_len
+    // (bottom-right aligned).  Rows left without keys give O = 0,
+    // Mi = -inf, Li = 0.
+    const int* kv_lens; // [B] or null (all kv_len)
+    int causal;         // 0 / 1
+    int q_len;
+    int heads_kv;       // H_kv: group index -> batch index
 };
+
+// Keys of the sequence that KV-head group `grp` belongs to, clamped to
+// [0, kv_len].
+__device__ __forceinline__ int batch_kv_len(const AttnParams& p, int grp) {
+    if (!p.kv_lens) return p.kv_len;
+    return min(max(p.kv_lens[grp / p.heads_kv], 0), p.kv_len);
+}
+
+// Number of leading keys visible to query index qi (0 <= qi < q_len) of a
+// sequence with kvb keys.
+__device__ __forceinline__ int row_kv_limit(const AttnParams& p, int kvb, int qi) {
+    if (!p.causal) return kvb;
+    return min(max(qi + kvb - p.q_len + 1, 0), kvb);
+}
+
+// Smallest and largest query index among group rows [r0, r1] (r0 <= r1);
+// group row r holds query index r % q_len.
+__device__ __forceinline__ void qi_range(int r0, int r1, int q_len, int& lo, int& hi) {
+    if (r0 / q_len != r1 / q_len) {
+        lo = 0;
+        hi = q_len - 1;
+    } else {
+        lo = r0 % q_len;
+        hi = r1 % q_len;
+    }
+}
 
 // ---------------------------------------------------------------------------
 // Small device helpers.
@@ -279,14 +314,18 @@ __device__ __forceinline__ void softmax_update(f32x16 (&s)[NSB], RowState& st,
     const float mt = mx * scale_log2;
     const bool need = mt > st.m + kLazyRescaleLog2;
     if (__any(need)) {
+        // Lanes that keep their max scale by exactly 1 (also when it is still
+        // -inf: exp2(-inf - -inf) would be NaN).
         const float mnew = need ? mt : st.m;
-        const float alpha = exp2_hw(st.m - mnew);
+        const float alpha = need ? exp2_hw(st.m - mt) : 1.0f;
         st.l *= alpha;
 #pragma unroll
         for (int td = 0; td < NTD; ++td) o[td] *= alpha;
         st.m = mnew;
     }
-    const float neg_m = -st.m;
+    // A row that has seen no key yet (all masked) keeps m = -inf: exponents
+    // must then give P = 0, not NaN.
+    const float neg_m = st.m == -INFINITY ? 0.f : -st.m;
     const f16x2 ones = {(f16)1.0f, (f16)1.0f};
     float sum[2] = {0.f, 0.f};
 #pragma unroll
@@ -463,8 +502,10 @@ __device__ __forceinline__ void block_update_max(RowState& st, float mx, float s
     const float mt = mx * scale_log2;
     const bool need = mt > st.m + kLazyRescaleLog2;
     if (__any(need)) {
+        // Lanes that keep their max scale by exactly 1 (also when it is still
+        // -inf, a fully masked row: exp2(-inf - -inf) would be NaN).
         const float mnew = need ? mt : st.m;
-        const float alpha = exp2_hw(st.m - mnew);
+        const float alpha = need ? exp2_hw(st.m - mt) : 1.0f;
         st.l *= alpha;
 #pragma unroll
         for (int td = 0; td < NTD; ++td) o[td] *= alpha;
@@ -472,7 +513,9 @@ __device__ __forceinline__ void block_update_max(RowState& st, float mx, float s
     }
 }
 
-template <int D>
+// kMask: causal masking and/or per-sequence key counts (p.causal,
+// p.kv_lens); without it every row sees keys [0, kv_len).
+template <int D, bool kMask>
 __global__ __launch_bounds__(PrefillCfg<D>::kThreads, PrefillCfg<D>::kWavesPerEU)
 void kf_attn_prefill_kernel(AttnParams p) {
     constexpr int BC = PrefillCfg<D>::BC;
@@ -496,13 +539,38 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
-    const int rt = blk % p.row_tiles;
+    int rt = blk % p.row_tiles;
     const int grp = blk / p.row_tiles;
     const int R = p.rows_per_group;
     const int kv_len = p.kv_len;
-    const int ntiles = (kv_len + BC - 1) / BC;    // 32-row tiles
-    const int nstages = (kv_len + SR - 1) / SR;   // LDS stages
     const float c = p.scale_log2;
+    // Causal: each XCD receives the row tiles of its groups in descending
+    // order, longest (most keys) first.
+    if (kMask && p.causal) rt = p.row_tiles - 1 - rt;
+
+    // Keys this workgroup needs (blk_lim) and, per wave, the smallest row
+    // limit (below it no masking is needed).
+    int kvb = kv_len, blk_lim = kv_len, wave_min = kv_len;
+    if constexpr (kMask) {
+        kvb = batch_kv_len(p, grp);
+        blk_lim = wave_min = kvb;
+        if (p.causal) {
+            const int q_len = p.q_len;
+            const int r0 = rt * kPrefillRows, r1 = min(R, r0 + kPrefillRows) - 1;
+            int lo, hi;
+            qi_range(r0, r1, q_len, lo, hi);
+            blk_lim = row_kv_limit(p, kvb, hi);
+            const int w0 = r0 + wave * 32;
+            if (w0 < R) {
+                qi_range(w0, min(R, w0 + 32) - 1, q_len, lo, hi);
+                wave_min = row_kv_limit(p, kvb, lo);
+            } else {
+                wave_min = blk_lim;
+            }
+        }
+    }
+    const int ntiles = (blk_lim + BC - 1) / BC;   // 32-row tiles
+    const int nstages = (blk_lim + SR - 1) / SR;  // LDS stages
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
     const char* Kh = reinterpret_cast<const char*>(p.K + (size_t)grp * kv_len * D);
@@ -638,10 +706,33 @@ void kf_attn_prefill_kernel(AttnParams p) {
         return sum;
     };
 
+    const int row = rt * kPrefillRows + wave * 32 + (lane & 31);
+    if (kMask && ntiles == 0) {
+        // No key for any row of this workgroup (whole-workgroup uniform).
+        if (row < R) {
+            float* Orow = p.O + ((size_t)grp * R + row) * D;
+#pragma unroll
+            for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int d = 32 * td + 8 * i + 4 * g;
+                    if (d < D) *reinterpret_cast<f32x4*>(Orow + d) = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+            if (g == 0) {
+                const size_t ri = (size_t)grp * R + row;
+                if (p.Mi) p.Mi[ri] = -INFINITY;
+                if (p.Li) p.Li[ri] = 0.f;
+            }
+        }
+        return;
+    }
+    // This lane's query row sees keys [0, lim_lane) (padding rows: blk_lim).
+    int lim_lane = kv_len;
+    if constexpr (kMask) lim_lane = row < R ? row_kv_limit(p, kvb, row % p.q_len) : blk_lim;
+
     // ---- Prologue: stage 0 (and 1 when pipelined) in flight, Q fragments, S(0). ----
     issue_stage(buf0, 0);
     if (kPipe && nstages > 1) issue_stage(buf1, SR);
-    const int row = rt * kPrefillRows + wave * 32 + (lane & 31);
     f16x8 qf[kNKK];
     load_q_frags<D>(Qg, row, R, lane, qf);
     if constexpr (D < 32) {
@@ -656,8 +747,11 @@ void kf_attn_prefill_kernel(AttnParams p) {
     for (int td = 0; td < kNTD; ++td) o[td] = f32x16{};
     f32x16 sc[kNSB];
     qk(buf0, qf, sc);
-    if (BC > kv_len) block_mask<kNSB>(sc, kv_len, lane);
+    if (BC > wave_min) block_mask<kNSB>(sc, lim_lane, lane);
     block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, o);
+    // Exponent offset; a row with no key yet (masked) keeps m = -inf and
+    // must get P = 0, not NaN.
+    auto neg_m = [&]() { return (kMask && st.m == -INFINITY) ? 0.f : -st.m; };
 
     // ---- One pipelined tile; S(t) and its running max are ready on entry.
     //   barrier; LDS-DMA of stage t+2
@@ -675,10 +769,10 @@ void kf_attn_prefill_kernel(AttnParams p) {
             if (t + 1 < ntiles) issue_stage(const_cast<char*>(nxt), (t + 1) * BC);
             if (t > 0) {
                 qk(cur, qf, sc);
-                if ((t + 1) * BC > kv_len) block_mask<kNSB>(sc, kv_len - t * BC, lane);
+                if ((t + 1) * BC > wave_min) block_mask<kNSB>(sc, lim_lane - t * BC, lane);
                 block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, o);
             }
-            st.l += softmax_exp(sc, -st.m, pp);
+            st.l += softmax_exp(sc, neg_m(), pp);
             pv(cur, pp, o);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();  // stage t+1 landed; every wave is done with stage t
@@ -695,15 +789,15 @@ void kf_attn_prefill_kernel(AttnParams p) {
         }
         f32x16 sn[kNSB];
         qk(nxt, qf, sn);
-        st.l += softmax_exp(sc, -st.m, pp);
+        st.l += softmax_exp(sc, neg_m(), pp);
         pv(cur, pp, o);
         float mx = block_rowmax<kNSB>(sn);
         if (t + 1 < ntiles) {
-            if ((t + 2) * BC > kv_len) {  // S(t+1) is the partial last tile
+            if ((t + 2) * BC > wave_min) {  // S(t+1) needs masking (tail / causal)
                 // Keep this a branch: if-converted, the compares and selects
                 // of the mask would run on every tile.
                 asm volatile("" ::: "memory");
-                block_mask<kNSB>(sn, kv_len - (t + 1) * BC, lane);
+                block_mask<kNSB>(sn, lim_lane - (t + 1) * BC, lane);
                 mx = block_rowmax<kNSB>(sn);
             }
             block_update_max<kNTD>(st, mx, c, o);
@@ -747,8 +841,9 @@ void kf_attn_prefill_kernel(AttnParams p) {
 
     // ---- Epilogue: combine the two half-row partial sums, normalise, store. ----
     const float l = st.l + __shfl_xor(st.l, 32);
+    const bool empty = kMask && !(l > 0.f);  // no visible key
     if (row < R) {
-        const float inv = 1.0f / l;
+        const float inv = empty ? 0.f : 1.0f / l;
         float* Orow = p.O + ((size_t)grp * R + row) * D;
 #pragma unroll
         for (int td = 0; td < kNTD; ++td)
@@ -764,7 +859,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
         if (g == 0) {
             const size_t ri = (size_t)grp * R + row;
             if (p.Mi) p.Mi[ri] = st.rmax * p.scale;
-            if (p.Li) p.Li[ri] = l * exp2_hw(st.m - st.rmax * p.scale_log2);
+            if (p.Li) p.Li[ri] = empty ? 0.f : l * exp2_hw(st.m - st.rmax * p.scale_log2);
         }
     }
 }
@@ -806,8 +901,13 @@ void kf_attn_decode_kernel(AttnParams p) {
     const int grp = blk / p.n_splits;
     const int R = p.rows_per_group;
     const int kv_len = p.kv_len;
+    // Keys of this sequence; with causal masking row r (query index
+    // r % q_len) sees the first row_kv_limit(...) of them, at least
+    // kvb - q_len + 1 (the rows of a group cover every query index).
+    const int kvb = batch_kv_len(p, grp);
     const int s0 = split * p.kv_per_split;
-    const int s1 = min(kv_len, s0 + p.kv_per_split);
+    const int s1 = min(kvb, s0 + p.kv_per_split);
+    const int lim_min = p.causal ? max(kvb - p.q_len + 1, 0) : kvb;
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
     const uint16_t* Kh = p.K + (size_t)grp * kv_len * D;
@@ -816,6 +916,7 @@ void kf_attn_decode_kernel(AttnParams p) {
     const int row = lane & 31;
     f16x8 qf[D / 16];
     load_q_frags<D>(Qg, row, R, lane, qf);
+    const int lim_lane = row < R ? row_kv_limit(p, kvb, row % p.q_len) : kvb;
 
     f16* Ks = reinterpret_cast<f16*>(smem_raw) + wave * G::kStageHalfs;
     f16* Vt = Ks + G::kKHalfs;
@@ -840,8 +941,8 @@ void kf_attn_decode_kernel(AttnParams p) {
 
         f32x16 s[1];
         s[0] = qk_block<D, kDecodeStage>(Ks, 0, qf, lane);
-        if (kv0 + kDecodeStage > s1) {
-            const int lim = s1 - kv0;
+        if (kv0 + kDecodeStage > min(s1, lim_min)) {
+            const int lim = min(s1, lim_lane) - kv0;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 if (acc_row(r, lane) >= lim) s[0][r] = -INFINITY;
@@ -898,7 +999,7 @@ void kf_attn_decode_kernel(AttnParams p) {
             l += wt[w] * Lb[w * 32 + mrow];
         }
         const bool final_out = p.n_splits == 1;
-        const float inv = final_out ? 1.0f / l : 1.0f;
+        const float inv = final_out ? (l > 0.f ? 1.0f / l : 0.f) : 1.0f;
         // Final rows go to O; split partials to [grp][split][row][D].
         const size_t ri = (size_t)grp * R + mrow;
         const size_t pi = ((size_t)grp * p.n_splits + split) * R + mrow;
@@ -967,8 +1068,9 @@ void kf_attn_split_merge_kernel(AttnParams p) {
     __syncthreads();
     m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
     float lsum = 0.f;
+    const bool none = m == -INFINITY;  // no split saw a key for this row
     for (int k = tid; k < ns; k += kMergeThreads) {
-        const float w = exp2_hw((s_w[k] - m) * kLog2e);
+        const float w = none ? 0.f : exp2_hw((s_w[k] - m) * kLog2e);
         s_w[k] = w;
         lsum += w * p.Lpart[base + (size_t)k * R];
     }
@@ -999,7 +1101,7 @@ void kf_attn_split_merge_kernel(AttnParams p) {
         f32x4 t = s_acc[0][tid];
 #pragma unroll
         for (int j = 1; j < kLanes; ++j) t += s_acc[j][tid];
-        *reinterpret_cast<f32x4*>(p.O + (size_t)row * D + 4 * tid) = t * (1.0f / l);
+        *reinterpret_cast<f32x4*>(p.O + (size_t)row * D + 4 * tid) = t * (l > 0.f ? 1.0f / l : 0.f);
         if (tid == 0) {
             if (p.Mi) p.Mi[row] = m;
             if (p.Li) p.Li[row] = l;

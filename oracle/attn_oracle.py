@@ -159,17 +159,41 @@ def _check_shapes(Q, K, V):
     return B, H_q, H_kv, q_len, kv_len, D
 
 
-def sdpa(Q, K, V, acc=np.float64):
+def key_limits(q_len, kv_len, causal=False, kv_lens=None, B=1):
+    """Visible keys per (batch, query index): an int array [B, q_len].
+
+    Sequence b uses its first kv_b = clip(kv_lens[b], 0, kv_len) keys (all
+    kv_len when kv_lens is None); with ``causal`` query i sees keys
+    j <= i + kv_b - q_len (bottom-right aligned), i.e. the first
+    clip(i + kv_b - q_len + 1, 0, kv_b).  The semantics of kf_attn_fwd_ex;
+    the reference has no masking (kernels/flash_attn.cu:384-585).
+    """
+    if kv_lens is None:
+        kvb = np.full(B, kv_len, dtype=np.int64)
+    else:
+        kvb = np.clip(np.asarray(kv_lens, dtype=np.int64).reshape(B), 0, kv_len)
+    lim = np.repeat(kvb[:, None], q_len, axis=1)
+    if causal:
+        i = np.arange(q_len, dtype=np.int64)[None, :]
+        lim = np.clip(i + kvb[:, None] - q_len + 1, 0, kvb[:, None])
+    return lim
+
+
+def sdpa(Q, K, V, acc=np.float64, causal=False, kv_lens=None):
     """Exact attention with GQA grouping; returns (O, Mi, Li).
 
     h_kv = h_q // (H_q // H_kv) (kernels/flash_attn.cu:406,
     kernel_models/flash_attn.py:259).  s = q.k * (1/sqrt(D)); Mi = max_j s;
     Li = sum_j exp(s - Mi); O = sum_j exp(s - Mi) v_j / Li.  Computed in
     ``acc`` precision (fp64 by default) from whatever values Q/K/V hold.
+    With ``causal`` / ``kv_lens`` only the keys of key_limits() enter each
+    row; a row that sees none gets O = 0, Mi = -inf, Li = 0.
     """
     B, H_q, H_kv, q_len, kv_len, D = _check_shapes(Q, K, V)
     ratio = H_q // H_kv
     scale = acc(1.0) / np.sqrt(acc(D))
+    masked = causal or kv_lens is not None
+    lim = key_limits(q_len, kv_len, causal, kv_lens, B) if masked else None
     O = np.empty((B, H_q, q_len, D), dtype=acc)
     M = np.empty((B, H_q, q_len), dtype=acc)
     L = np.empty((B, H_q, q_len), dtype=acc)
@@ -180,6 +204,17 @@ def sdpa(Q, K, V, acc=np.float64):
             k = np.asarray(K[b, hk], dtype=acc)
             v = np.asarray(V[b, hk], dtype=acc)
             s = (q @ k.T) * scale
+            if masked:
+                visible = np.arange(kv_len)[None, :] < lim[b][:, None]
+                s = np.where(visible, s, -np.inf)
+                empty = lim[b] == 0
+                m = np.where(empty, 0.0, s.max(axis=1))
+                p = np.exp(s - m[:, None])
+                l = p.sum(axis=1)
+                O[b, h] = (p @ v) / np.where(empty, 1.0, l)[:, None]
+                M[b, h] = np.where(empty, -np.inf, m)
+                L[b, h] = l
+                continue
             m = s.max(axis=1)
             p = np.exp(s - m[:, None])
             l = p.sum(axis=1)

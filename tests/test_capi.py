@@ -96,6 +96,26 @@ def test_workspace_required_for_split_decode():
     assert _fwd(ws=FAKE_WS + 16, ws_bytes=pl.workspace_bytes, **args) == kf.KF_ERR_ALIGN
 
 
+def _fwd_ex(kv_lens=0, flags=0, **kw):
+    a = dict(B=1, q=4, kv=64, H_q=8, H_kv=2, D=128)
+    a.update(kw)
+    return kf.attn_fwd_ex_ptr(FAKE, FAKE, FAKE, FAKE, 0, 0, a["B"], a["q"], a["kv"], a["H_q"],
+                              a["H_kv"], a["D"], kv_lens, flags)
+
+
+def test_fwd_ex_validation():
+    assert _fwd_ex(flags=2) == kf.KF_ERR_FLAGS
+    assert _fwd_ex(flags=-1) == kf.KF_ERR_FLAGS
+    assert _fwd_ex(kv_lens=FAKE + 2) == kf.KF_ERR_ALIGN        # int array: 4-byte aligned
+    assert _fwd_ex(D=96, flags=kf.KF_ATTN_CAUSAL) == kf.KF_ERR_HEAD_DIM
+    assert _fwd_ex(H_kv=3, flags=kf.KF_ATTN_CAUSAL) == kf.KF_ERR_GQA
+    assert _fwd_ex(q=0, kv_lens=FAKE) == kf.KF_ERR_SIZE
+    assert kf.attn_fwd_ex_ptr(0, FAKE, FAKE, FAKE, 0, 0, 1, 4, 64, 8, 2, 128, 0,
+                              kf.KF_ATTN_CAUSAL) == kf.KF_ERR_NULL
+    # Split decode still needs its workspace with masking.
+    assert _fwd_ex(q=1, kv=4096, H_q=32, H_kv=8, flags=kf.KF_ATTN_CAUSAL) == kf.KF_ERR_WORKSPACE
+
+
 def test_reference_launcher_rejects_like_the_reference():
     # tests/test_flash_attn.cu:96-100: unsupported D -> cudaErrorInvalidValue.
     assert kf.launch_flash_attn(FAKE, FAKE, FAKE, FAKE, 1, 64, 8, 2, 96) == kf.HIP_ERROR_INVALID_VALUE
@@ -104,8 +124,8 @@ def test_reference_launcher_rejects_like_the_reference():
 
 
 def test_status_strings_distinct(lib):
-    texts = [kf.status_string(s) for s in range(8)]
-    assert len(set(texts)) == 8
+    texts = [kf.status_string(s) for s in range(9)]
+    assert len(set(texts)) == 9
     assert kf.status_string(99) == "unknown status"
 
 

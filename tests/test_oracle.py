@@ -297,3 +297,85 @@ def test_flops_and_bytes_formulas():
     assert orc.attn_flops(1, 32, 4096, 4096, 128) == 274877906944
     assert orc.attn_bytes(1, 32, 8, 1, 4096, 128) == 16801792
     assert orc.attn_bytes(32, 32, 8, 1, 8192, 128) == 1074528256
+
+
+# ---------------------------------------------------------------------------
+# Key masking (causal, per-sequence key counts): the semantics of
+# kf_attn_fwd_ex, pinned against the already-pinned unmasked sdpa on
+# truncated inputs, torch's own causal attention, and closed forms.
+# ---------------------------------------------------------------------------
+def test_key_limits_closed_forms():
+    np.testing.assert_array_equal(orc.key_limits(4, 4, causal=True)[0], [1, 2, 3, 4])
+    np.testing.assert_array_equal(orc.key_limits(3, 5, causal=True)[0], [3, 4, 5])
+    np.testing.assert_array_equal(orc.key_limits(5, 3, causal=True)[0], [0, 0, 1, 2, 3])
+    np.testing.assert_array_equal(orc.key_limits(2, 9, kv_lens=[4, 0, 99], B=3),
+                                  [[4, 4], [0, 0], [9, 9]])
+    np.testing.assert_array_equal(orc.key_limits(3, 9, causal=True, kv_lens=[2, 9], B=2),
+                                  [[0, 1, 2], [7, 8, 9]])
+    np.testing.assert_array_equal(orc.key_limits(1, 7, causal=True)[0], [7])  # decode: no-op
+
+
+@pytest.mark.parametrize("q_len,kv_len", [(6, 6), (4, 9), (7, 3)])
+def test_causal_rows_equal_attention_over_their_prefix(q_len, kv_len):
+    Q, K, V = _rand((1, 4, q_len, 16), 21), _rand((1, 2, kv_len, 16), 22), _rand((1, 2, kv_len, 16), 23)
+    O, M, L = orc.sdpa(Q, K, V, causal=True)
+    for i in range(q_len):
+        n = i + kv_len - q_len + 1
+        if n <= 0:
+            assert (O[:, :, i] == 0).all() and np.isneginf(M[:, :, i]).all() and (L[:, :, i] == 0).all()
+            continue
+        Op, Mp, Lp = orc.sdpa(Q[:, :, i:i + 1], K[:, :, :n], V[:, :, :n])
+        np.testing.assert_allclose(O[:, :, i:i + 1], Op, rtol=1e-13, atol=1e-15)
+        np.testing.assert_allclose(M[:, :, i:i + 1], Mp, rtol=1e-13)
+        np.testing.assert_allclose(L[:, :, i:i + 1], Lp, rtol=1e-13)
+
+
+def test_causal_first_row_is_v0():
+    Q, K, V = _rand((2, 4, 5, 32), 31), _rand((2, 4, 5, 32), 32), _rand((2, 4, 5, 32), 33)
+    O, _, L = orc.sdpa(Q, K, V, causal=True)
+    np.testing.assert_array_equal(O[:, :, 0], V[:, :, 0])
+    np.testing.assert_array_equal(L[:, :, 0], 1.0)
+
+
+@pytest.mark.parametrize("q_len,kv_len", [(8, 8), (5, 11)])
+def test_causal_matches_torch(q_len, kv_len):
+    torch = pytest.importorskip("torch")
+    Q, K, V = _rand((2, 4, q_len, 16), 41), _rand((2, 2, kv_len, 16), 42), _rand((2, 2, kv_len, 16), 43)
+    tq = torch.from_numpy(Q)
+    tk = torch.from_numpy(K).repeat_interleave(2, dim=1)
+    tv = torch.from_numpy(V).repeat_interleave(2, dim=1)
+    if q_len == kv_len:
+        ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=True)
+    else:  # bottom-right alignment as a boolean tril mask
+        mask = torch.ones(q_len, kv_len, dtype=torch.bool).tril(diagonal=kv_len - q_len)
+        ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=mask)
+    O, _, _ = orc.sdpa(Q, K, V, causal=True)
+    np.testing.assert_allclose(O, ref.numpy(), rtol=1e-11, atol=1e-12)
+
+
+def test_kv_lens_equal_truncated_sequences():
+    Q, K, V = _rand((3, 4, 6, 16), 51), _rand((3, 2, 10, 16), 52), _rand((3, 2, 10, 16), 53)
+    lens = [10, 1, 0]
+    O, M, L = orc.sdpa(Q, K, V, kv_lens=lens)
+    for b, n in enumerate(lens):
+        if n == 0:
+            assert (O[b] == 0).all() and np.isneginf(M[b]).all() and (L[b] == 0).all()
+            continue
+        Ob, Mb, Lb = orc.sdpa(Q[b:b + 1], K[b:b + 1, :, :n], V[b:b + 1, :, :n])
+        np.testing.assert_allclose(O[b:b + 1], Ob, rtol=1e-13, atol=1e-15)
+        np.testing.assert_allclose(M[b:b + 1], Mb, rtol=1e-13)
+    # kv_len = 1 keeps the closed form O = V_0.
+    O1, _, _ = orc.sdpa(Q, K, V, kv_lens=[1, 1, 1])
+    np.testing.assert_array_equal(O1, np.repeat(V[:, :, :1], 2, axis=1).repeat(6, axis=2))
+
+
+def test_planted_mask_off_by_one_is_caught(monkeypatch):
+    real = orc.key_limits
+
+    def shifted(*a, **kw):
+        return np.maximum(real(*a, **kw) - 1, 0)
+
+    monkeypatch.setattr(orc, "key_limits", shifted)
+    Q, K, V = _rand((1, 2, 5, 16), 61), _rand((1, 2, 5, 16), 62), _rand((1, 2, 5, 16), 63)
+    O, _, _ = orc.sdpa(Q, K, V, causal=True)
+    assert not np.array_equal(O[:, :, 0], V[:, :, 0]), "off-by-one mask slipped through"
