@@ -544,9 +544,20 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const int R = p.rows_per_group;
     const int kv_len = p.kv_len;
     const float c = p.scale_log2;
-    // Causal: each XCD receives the row tiles of its groups in descending
-    // order, longest (most keys) first.
-    if (kMask && p.causal) rt = p.row_tiles - 1 - rt;
+    // Causal: a row tile's work grows with its position inside its head.
+    // Each XCD receives its groups' row tiles longest first, so late, short
+    // tiles fill the CUs that finish early: logical k -> position
+    // T - 1 - k / heads of head k % heads, T = row tiles per head (when
+    // tiles do not straddle heads; otherwise plain descending order).
+    if (kMask && p.causal) {
+        const int q_len = p.q_len;
+        if (q_len % kPrefillRows == 0) {
+            const int T = q_len / kPrefillRows, heads = R / q_len;
+            rt = (rt % heads) * T + (T - 1 - rt / heads);
+        } else {
+            rt = p.row_tiles - 1 - rt;
+        }
+    }
 
     // Keys this workgroup needs (blk_lim) and, per wave, the smallest row
     // limit (below it no masking is needed).
