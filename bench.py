@@ -18,6 +18,11 @@ half of the metric):
   * ``prefill_causal`` -- the configs[2] shape with the causal mask of
                      kf_attn_fwd_ex; FLOPs count only the visible pairs,
                      4*B*H_q*D*S(S+1)/2.
+  * ``decode_paged`` -- the configs[4] decode over a paged cache
+                     (kf_attn_decode_paged): 16-row pages scattered over a
+                     pool twice the needed size (the reference's worst-case
+                     fragmentation, bench_flash_attn2.py:153-215); bytes =
+                     configs[4]'s plus the block table.
   * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep)
                      and the MQA D=64 configs[3].
 
@@ -164,6 +169,68 @@ def parity_spot_check(torch, runner, heads, causal=False):
             "atol": orc.ATOL, "rtol": orc.RTOL, "ok": True}
 
 
+def run_paged_decode(torch, kf, steps, warmup, check, B=32, kv=8192, H_q=32, H_kv=8, D=128,
+                     page_size=16):
+    """configs[4] decode over a fragmented paged cache; returns a result dict."""
+    max_pages = kv // page_size
+    num_pages = 2 * B * max_pages
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4242)
+    Kp = torch.randn((num_pages, H_kv, page_size, D), generator=g, device="cuda").half()
+    Vp = torch.randn((num_pages, H_kv, page_size, D), generator=g, device="cuda").half()
+    Q = torch.randn((B, H_q, 1, D), generator=g, device="cuda").half()
+    table = torch.randperm(num_pages, generator=g, device="cuda")[:B * max_pages] \
+        .to(torch.int32).reshape(B, max_pages).contiguous()
+    lens = torch.full((B,), kv, dtype=torch.int32, device="cuda")
+    O = torch.empty((B, H_q, 1, D), dtype=torch.float32, device="cuda")
+    need = kf.paged_workspace_bytes(B, 1, H_q, H_kv, D, page_size, max_pages)
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+    lib = kf.load_library()
+    stream = torch.cuda.current_stream()
+    args = (Q.data_ptr(), Kp.data_ptr(), Vp.data_ptr(), table.data_ptr(), lens.data_ptr(),
+            O.data_ptr(), None, None, B, 1, H_q, H_kv, D, page_size, max_pages, num_pages, 0,
+            ws.data_ptr(), need, stream.cuda_stream)
+
+    class _R:
+        stream = None
+
+        def launch(self):
+            st = lib.kf_attn_decode_paged(*args)
+            if st != 0:
+                raise RuntimeError(f"kf_attn_decode_paged failed: {kf.status_string(st)}")
+
+    r = _R()
+    r.stream = stream
+    ms, kern_mean, _ = time_steps(torch, r, steps, warmup)
+    by = nbytes(B, H_q, H_kv, 1, kv, D) + table.numel() * 4
+    out = {"config": f"configs[4] over a paged cache: B={B} KV={kv} page_size={page_size}, "
+                     f"pages randomly placed in a {num_pages}-page pool",
+           "latency_us": round(ms * 1e3, 2), "hbm_gbs": round(by / (ms * 1e6), 1),
+           "launch_us_mean": round(kern_mean * 1e3, 2), "bytes_per_launch": by,
+           "roofline": {"bound": "hbm", "achieved": round(by / (ms * 1e6), 1),
+                        "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                        "frac": round(by / (ms * 1e6) / PEAK_HBM_GBS, 4)}}
+    if check:
+        from oracle import attn_oracle as orc
+        import numpy as np
+        tb = table.cpu().numpy()
+        heads = [(0, 0), (B - 1, H_q - 1)]
+        worst = (0.0, 0.0)
+        for b, h in heads:
+            hk = h // (H_q // H_kv)
+            ids = torch.from_numpy(tb[b].astype(np.int64)).cuda()
+            Kc = Kp[ids][:, hk].reshape(1, 1, kv, D).cpu().numpy()
+            Vc = Vp[ids][:, hk].reshape(1, 1, kv, D).cpu().numpy()
+            ref, _, _ = orc.sdpa(Q[b:b + 1, h:h + 1].cpu().numpy(), Kc, Vc)
+            ok, mx, rel = orc.within_tolerance(O[b:b + 1, h:h + 1].cpu().numpy(), ref)
+            if not ok:
+                raise AssertionError(f"paged bench parity failed on ({b},{h}): {mx} {rel}")
+            worst = (max(worst[0], mx), max(worst[1], rel))
+        out["parity"] = {"heads": [list(x) for x in heads], "max_abs": worst[0],
+                         "rel_l2": worst[1], "atol": orc.ATOL, "rtol": orc.RTOL, "ok": True}
+    return out
+
+
 def cpu_baseline(seconds_target=15.0):
     """Time the NumPy restatement of the reference's CPU path (fp32 SDPA per
     head) on a bounded sample of the headline workload: a subset of the 32
@@ -221,7 +288,8 @@ def main():
     ap.add_argument("--decode-sets", type=int, default=40,
                     help="distinct Q/K/V sets rotated through for the KV=4096 decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "prefill_causal", "decode", "decode_b32", "copy"],
+    ap.add_argument("--only", choices=["prefill", "prefill_causal", "decode", "decode_b32",
+                                       "decode_paged", "copy"],
                     default=None,
                     help="run one workload only (for rocprof counter passes); prints no JSON")
     args = ap.parse_args()
@@ -318,6 +386,12 @@ def main():
         results["decode_b32"]["parity"] = parity_spot_check(torch, rb, [(0, 0), (31, 31)])
         del rb
 
+    if args.only in (None, "decode_paged"):
+        print("bench: paged decode B=32 KV=8192 page 16", file=sys.stderr, flush=True)
+        results["decode_paged"] = run_paged_decode(torch, kf, steps, warmup, args.only is None)
+        if args.only:
+            return
+
     print("bench: sweep", file=sys.stderr, flush=True)
     sweep = [run_prefill(S) for S in (512, 1024, 2048)]
     sweep.append(run_prefill(2048, H_kv=1, D=64))
@@ -383,6 +457,7 @@ def main():
             "parity": b32["parity"],
         },
         "prefill_causal": results["prefill_causal"],
+        "decode_paged": results["decode_paged"],
         "sweep": sweep,
         "parity": pre.get("parity"),
     }

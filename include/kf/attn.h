@@ -124,6 +124,35 @@ int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, float* O,
                    const int* kv_lens, int flags,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Decode over a paged K/V cache, the block-table gather fused into the
+ * split-KV decode kernel.  Replaces the gather + attention of the
+ * reference's paged comparison (reference_benchmarks/bench_flash_attn2.py:
+ * 153-215: pools [pool_blocks, H_kv, block_size, D], block ids per page),
+ * which it names as the job of a specialised paged-attention kernel; the
+ * reference has no such kernel.
+ *
+ * K_pages, V_pages: [num_pages, H_kv, page_size, D] fp16 page pools.
+ * block_table: device int [B, max_pages_per_seq]; key j of sequence b is row
+ *   j % page_size of page block_table[b * max_pages_per_seq + j / page_size].
+ *   An id outside [0, num_pages) contributes no keys: the kernel never reads
+ *   outside the pools.
+ * kv_lens: device int [B], keys of each sequence, clamped to
+ *   [0, max_pages_per_seq * page_size]; required.
+ * page_size: a power of two in [16, 2^20].
+ * Q, O, row_max, row_sumexp, flags (KF_ATTN_CAUSAL) as in kf_attn_fwd_ex,
+ * with kv_len = max_pages_per_seq * page_size.  The decode path only: at
+ * most 32 query rows per KV head ((H_q / H_kv) * q_len <= 32), else
+ * KF_ERR_SIZE.  Workspace: kf_attn_decode_paged_workspace_bytes() bytes,
+ * 256-byte aligned, no initialisation. */
+size_t kf_attn_decode_paged_workspace_bytes(int B, int q_len, int H_q, int H_kv, int D,
+                                            int page_size, int max_pages_per_seq);
+int kf_attn_decode_paged(const void* Q, const void* K_pages, const void* V_pages,
+                         const int* block_table, const int* kv_lens,
+                         float* O, float* row_max, float* row_sumexp,
+                         int B, int q_len, int H_q, int H_kv, int D,
+                         int page_size, int max_pages_per_seq, int num_pages, int flags,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 /* The reference launcher's contract (tests/test_flash_attn.cu:52-113):
  * q_len = kv_len = S, scratch allocated and freed by the call, stream
  * synchronised before returning.  Returns a hipError_t value:

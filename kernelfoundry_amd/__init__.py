@@ -18,6 +18,9 @@ Interface, mirroring the reference harness (sviraaj/kernelfoundry):
 * ``attn_fwd(..., causal=True, kv_lens=...)`` / ``attn_fwd_ex_ptr(...)`` --
   kf_attn_fwd_ex: bottom-right-aligned causal masking and per-sequence key
   counts over a pre-allocated K/V cache (no reference counterpart).
+* ``attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, ...)`` --
+  kf_attn_decode_paged: decode over a paged K/V cache (page pools
+  [num_pages, H_kv, page_size, D] and a per-sequence block table).
 * ``plan(B, q_len, kv_len, H_q, H_kv, D)`` -- which kernels run, GPU-free.
 """
 from __future__ import annotations
@@ -32,7 +35,8 @@ __all__ = [
     "attn_fwd_ptr", "launch_flash_attn", "status_string", "exported_symbols",
     "KF_OK", "KF_ERR_HEAD_DIM", "KF_ERR_GQA", "KF_ERR_SIZE", "KF_ERR_NULL",
     "KF_ERR_WORKSPACE", "KF_ERR_ALIGN", "KF_ERR_HIP", "KF_ERR_FLAGS", "KF_ATTN_CAUSAL",
-    "PATH_NAMES", "attn_fwd_ex_ptr",
+    "PATH_NAMES", "attn_fwd_ex_ptr", "attn_decode_paged", "attn_decode_paged_ptr",
+    "paged_workspace_bytes",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -107,6 +111,10 @@ def load_library(path: str = LIB_PATH):
     lib.kf_attn_fwd.restype = i
     lib.kf_attn_fwd_ex.argtypes = [p, p, p, p, p, p] + [i] * 6 + [p, i, p, sz, p]
     lib.kf_attn_fwd_ex.restype = i
+    lib.kf_attn_decode_paged.argtypes = [p] * 8 + [i] * 9 + [p, sz, p]
+    lib.kf_attn_decode_paged.restype = i
+    lib.kf_attn_decode_paged_workspace_bytes.argtypes = [i] * 7
+    lib.kf_attn_decode_paged_workspace_bytes.restype = sz
     lib.kf_launch_flash_attn.argtypes = [p, p, p, p] + [i] * 5 + [p]
     lib.kf_launch_flash_attn.restype = i
     lib.kf_status_string.argtypes = [i]
@@ -156,6 +164,21 @@ def attn_fwd_ex_ptr(Q, K, V, O, Mi, Li, B, q_len, kv_len, H_q, H_kv, D, kv_lens=
     return int(load_library().kf_attn_fwd_ex(Q, K, V, O, Mi or None, Li or None, B, q_len,
                                              kv_len, H_q, H_kv, D, kv_lens or None, flags,
                                              workspace or None, workspace_bytes, stream or None))
+
+
+def paged_workspace_bytes(B, q_len, H_q, H_kv, D, page_size, max_pages_per_seq) -> int:
+    return int(load_library().kf_attn_decode_paged_workspace_bytes(B, q_len, H_q, H_kv, D,
+                                                                    page_size, max_pages_per_seq))
+
+
+def attn_decode_paged_ptr(Q, K_pages, V_pages, block_table, kv_lens, O, Mi, Li, B, q_len, H_q,
+                          H_kv, D, page_size, max_pages_per_seq, num_pages, flags=0, workspace=0,
+                          workspace_bytes=0, stream=0) -> int:
+    """kf_attn_decode_paged on raw device addresses (ints); returns the kf status."""
+    return int(load_library().kf_attn_decode_paged(
+        Q, K_pages, V_pages, block_table or None, kv_lens or None, O, Mi or None, Li or None,
+        B, q_len, H_q, H_kv, D, page_size, max_pages_per_seq, num_pages, flags,
+        workspace or None, workspace_bytes, stream or None))
 
 
 def launch_flash_attn(Q, K, V, O, B, S, H_q, H_kv, D, stream=0) -> int:
@@ -210,6 +233,57 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
                          KF_ATTN_CAUSAL if causal else 0,
                          workspace.data_ptr() if (need and workspace is not None) else 0,
                          need, stream.cuda_stream)
+    if st != KF_OK:
+        msg = status_string(st)
+        if st == KF_ERR_HIP:
+            msg += f" (hipError_t {load_library().kf_last_hip_error()})"
+        raise KfError(st, msg)
+    return (out, Mi, Li) if return_stats else out
+
+
+def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, return_stats=False,
+                      causal=False, workspace=None, stream=None):
+    """Decode over a paged K/V cache on torch GPU tensors.
+
+    Q [B, H_q, q_len, D] fp16; K_pages / V_pages [num_pages, H_kv, page_size,
+    D] fp16; block_table int32 [B, max_pages_per_seq]; kv_lens int32 [B].
+    Returns O [B, H_q, q_len, D] fp32 (and Mi, Li with ``return_stats``).
+    """
+    import torch
+
+    for t, name in ((Q, "Q"), (K_pages, "K_pages"), (V_pages, "V_pages")):
+        if t.dtype != torch.float16 or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float16 GPU tensor")
+    for t, name in ((block_table, "block_table"), (kv_lens, "kv_lens")):
+        if t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int32 GPU tensor")
+    B, H_q, q_len, D = Q.shape
+    num_pages, H_kv, page_size, Dk = K_pages.shape
+    if K_pages.shape != V_pages.shape or Dk != D:
+        raise ValueError("K_pages / V_pages must be [num_pages, H_kv, page_size, D]")
+    if block_table.dim() != 2 or block_table.shape[0] != B or kv_lens.numel() != B:
+        raise ValueError("block_table must be [B, max_pages_per_seq] and kv_lens [B]")
+    max_pages = block_table.shape[1]
+    if out is None:
+        out = torch.empty((B, H_q, q_len, D), dtype=torch.float32, device=Q.device)
+    Mi = Li = None
+    if return_stats:
+        Mi = torch.empty((B, H_q, q_len), dtype=torch.float32, device=Q.device)
+        Li = torch.empty_like(Mi)
+    need = paged_workspace_bytes(B, q_len, H_q, H_kv, D, page_size, max_pages)
+    if stream is None:
+        stream = torch.cuda.current_stream(Q.device)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=Q.device)
+        workspace.record_stream(stream)
+    st = attn_decode_paged_ptr(Q.data_ptr(), K_pages.data_ptr(), V_pages.data_ptr(),
+                               block_table.data_ptr(), kv_lens.data_ptr(), out.data_ptr(),
+                               Mi.data_ptr() if Mi is not None else 0,
+                               Li.data_ptr() if Li is not None else 0,
+                               B, q_len, H_q, H_kv, D, page_size, max_pages, num_pages,
+                               KF_ATTN_CAUSAL if causal else 0,
+                               workspace.data_ptr() if (need and workspace is not None) else 0,
+                               need, stream.cuda_stream)
     if st != KF_OK:
         msg = status_string(st)
         if st == KF_ERR_HIP:

@@ -111,11 +111,83 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
             kf::kf_attn_prefill_kernel<D, false><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
         return hipGetLastError();
     }
-    kf::kf_attn_decode_kernel<D><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+    if (prm.block_table)
+        kf::kf_attn_decode_kernel<D, true><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+    else
+        kf::kf_attn_decode_kernel<D, false><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || pl.path != KF_PATH_DECODE_SPLIT) return e;
     kf::kf_attn_split_merge_kernel<D><<<dim3(pl.rows_total), dim3(kf::kMergeThreads), 0, stream>>>(prm);
     return hipGetLastError();
+}
+
+// Shared tail of kf_attn_fwd_ex and kf_attn_decode_paged: pointer and
+// workspace checks, the common kernel parameters, the launches.  `prm`
+// arrives with the masking / paging fields already set.
+int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const void* V, float* O,
+        float* row_max, float* row_sumexp, int q_len, int kv_len, int H_kv, int D, int flags,
+        void* workspace, size_t workspace_bytes, void* stream) {
+    if ((flags & ~KF_ATTN_CAUSAL) != 0) return KF_ERR_FLAGS;
+    if (!Q || !K || !V || !O) return KF_ERR_NULL;
+    if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O)) return KF_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(prm.kv_lens) & 3u) != 0) return KF_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(prm.block_table) & 3u) != 0) return KF_ERR_ALIGN;
+    if (pl.ws_bytes > 0) {
+        if (!workspace || workspace_bytes < pl.ws_bytes) return KF_ERR_WORKSPACE;
+        if ((reinterpret_cast<uintptr_t>(workspace) & (kWsAlign - 1)) != 0) return KF_ERR_ALIGN;
+    }
+
+    prm.Q = static_cast<const uint16_t*>(Q);
+    prm.K = static_cast<const uint16_t*>(K);
+    prm.V = static_cast<const uint16_t*>(V);
+    prm.O = O;
+    prm.Mi = row_max;
+    prm.Li = row_sumexp;
+    if (pl.ws_bytes > 0) {
+        char* ws = static_cast<char*>(workspace);
+        prm.Opart = reinterpret_cast<float*>(ws + pl.ws_o_off);
+        prm.Mpart = reinterpret_cast<float*>(ws + pl.ws_m_off);
+        prm.Lpart = reinterpret_cast<float*>(ws + pl.ws_l_off);
+    }
+    prm.rows_per_group = pl.R;
+    prm.kv_len = kv_len;
+    prm.row_tiles = pl.row_tiles;
+    prm.n_splits = pl.n_splits;
+    prm.kv_per_split = pl.kv_per_split;
+    prm.rows_total = pl.rows_total;
+    const double scale = 1.0 / __builtin_sqrt((double)D);
+    prm.scale = 1.0f / __builtin_sqrtf((float)D);  // the reference's fp32 scale
+    prm.scale_log2 = (float)(scale * 1.4426950408889634);
+    prm.causal = (flags & KF_ATTN_CAUSAL) ? 1 : 0;
+    prm.q_len = q_len;
+    prm.heads_kv = H_kv;
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    switch (D) {
+        case 16: e = launch_all<16>(pl, prm, s); break;
+        case 64: e = launch_all<64>(pl, prm, s); break;
+        case 128: e = launch_all<128>(pl, prm, s); break;
+        default: e = launch_all<256>(pl, prm, s); break;
+    }
+    if (e != hipSuccess) return hip_fail(e);
+    return KF_OK;
+}
+
+// Paged geometry: page_size a power of two in [16, 2^20], positive counts,
+// key capacity max_pages_per_seq * page_size within int.  Returns the
+// status and, on success, log2(page_size) and the capacity.
+int paged_geometry(int page_size, int max_pages_per_seq, int num_pages, int* shift, int* cap) {
+    if (max_pages_per_seq <= 0 || num_pages <= 0) return KF_ERR_SIZE;
+    if (page_size < 16 || page_size > (1 << 20) || (page_size & (page_size - 1)) != 0)
+        return KF_ERR_SIZE;
+    const long long c = (long long)page_size * max_pages_per_seq;
+    if (c > INT_MAX) return KF_ERR_SIZE;
+    int sh = 0;
+    while ((1 << sh) < page_size) ++sh;
+    *shift = sh;
+    *cap = (int)c;
+    return KF_OK;
 }
 
 }  // namespace
@@ -157,52 +229,43 @@ int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, float* O, float*
     Plan pl;
     const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, &pl);
     if (st != KF_OK) return st;
-    if ((flags & ~KF_ATTN_CAUSAL) != 0) return KF_ERR_FLAGS;
-    if (!Q || !K || !V || !O) return KF_ERR_NULL;
-    if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O)) return KF_ERR_ALIGN;
-    if ((reinterpret_cast<uintptr_t>(kv_lens) & 3u) != 0) return KF_ERR_ALIGN;
-    if (pl.ws_bytes > 0) {
-        if (!workspace || workspace_bytes < pl.ws_bytes) return KF_ERR_WORKSPACE;
-        if ((reinterpret_cast<uintptr_t>(workspace) & (kWsAlign - 1)) != 0) return KF_ERR_ALIGN;
-    }
-
     kf::AttnParams prm{};
-    prm.Q = static_cast<const uint16_t*>(Q);
-    prm.K = static_cast<const uint16_t*>(K);
-    prm.V = static_cast<const uint16_t*>(V);
-    prm.O = O;
-    prm.Mi = row_max;
-    prm.Li = row_sumexp;
-    if (pl.ws_bytes > 0) {
-        char* ws = static_cast<char*>(workspace);
-        prm.Opart = reinterpret_cast<float*>(ws + pl.ws_o_off);
-        prm.Mpart = reinterpret_cast<float*>(ws + pl.ws_m_off);
-        prm.Lpart = reinterpret_cast<float*>(ws + pl.ws_l_off);
-    }
-    prm.rows_per_group = pl.R;
-    prm.kv_len = kv_len;
-    prm.row_tiles = pl.row_tiles;
-    prm.n_splits = pl.n_splits;
-    prm.kv_per_split = pl.kv_per_split;
-    prm.rows_total = pl.rows_total;
-    const double scale = 1.0 / __builtin_sqrt((double)D);
-    prm.scale = 1.0f / __builtin_sqrtf((float)D);  // the reference's fp32 scale
-    prm.scale_log2 = (float)(scale * 1.4426950408889634);
     prm.kv_lens = kv_lens;
-    prm.causal = (flags & KF_ATTN_CAUSAL) ? 1 : 0;
-    prm.q_len = q_len;
-    prm.heads_kv = H_kv;
+    return run(pl, prm, Q, K, V, O, row_max, row_sumexp, q_len, kv_len, H_kv, D, flags,
+               workspace, workspace_bytes, stream);
+}
 
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t e;
-    switch (D) {
-        case 16: e = launch_all<16>(pl, prm, s); break;
-        case 64: e = launch_all<64>(pl, prm, s); break;
-        case 128: e = launch_all<128>(pl, prm, s); break;
-        default: e = launch_all<256>(pl, prm, s); break;
-    }
-    if (e != hipSuccess) return hip_fail(e);
-    return KF_OK;
+size_t kf_attn_decode_paged_workspace_bytes(int B, int q_len, int H_q, int H_kv, int D,
+                                            int page_size, int max_pages_per_seq) {
+    int sh, cap;
+    if (paged_geometry(page_size, max_pages_per_seq, 1, &sh, &cap) != KF_OK) return 0;
+    Plan pl;
+    if (make_plan(B, q_len, cap, H_q, H_kv, D, &pl) != KF_OK || pl.path == KF_PATH_PREFILL)
+        return 0;
+    return pl.ws_bytes;
+}
+
+int kf_attn_decode_paged(const void* Q, const void* K_pages, const void* V_pages,
+                         const int* block_table, const int* kv_lens, float* O, float* row_max,
+                         float* row_sumexp, int B, int q_len, int H_q, int H_kv, int D,
+                         int page_size, int max_pages_per_seq, int num_pages, int flags,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    int sh, cap;
+    int st = paged_geometry(page_size, max_pages_per_seq, num_pages, &sh, &cap);
+    if (st != KF_OK) return st;
+    Plan pl;
+    st = make_plan(B, q_len, cap, H_q, H_kv, D, &pl);
+    if (st != KF_OK) return st;
+    if (pl.path == KF_PATH_PREFILL) return KF_ERR_SIZE;  // more than 32 query rows per KV head
+    if (!block_table || !kv_lens) return KF_ERR_NULL;
+    kf::AttnParams prm{};
+    prm.kv_lens = kv_lens;
+    prm.block_table = block_table;
+    prm.max_pages = max_pages_per_seq;
+    prm.page_shift = sh;
+    prm.num_pages = num_pages;
+    return run(pl, prm, Q, K_pages, V_pages, O, row_max, row_sumexp, q_len, cap, H_kv, D, flags,
+               workspace, workspace_bytes, stream);
 }
 
 int kf_launch_flash_attn(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,

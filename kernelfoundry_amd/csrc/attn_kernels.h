@@ -95,6 +95,14 @@ struct AttnParams {
     int causal;         // 0 / 1
     int q_len;
     int heads_kv;       // H_kv: group index -> batch index
+    // Paged K/V (kf_attn_decode_paged): K and V point to page pools
+    // [num_pages][H_kv][page_size][D]; key j of sequence b lives in page
+    // block_table[b * max_pages + j / page_size], row j % page_size.  A page
+    // id outside [0, num_pages) contributes no keys (it is never read).
+    const int* block_table;
+    int max_pages;      // block_table row length; kv_len = max_pages * page_size
+    int page_shift;     // log2(page_size), page_size >= 16
+    int num_pages;
 };
 
 // Keys of the sequence that KV-head group `grp` belongs to, clamped to
@@ -214,6 +222,39 @@ struct StageLoader {
             for (int r = 0; r < 4; ++r) {
                 const int kv = kv0 + 4 * grp + r;
                 v[i][r] = load16(Vh + (size_t)kv * D + c * 8, in && kv < kv_end);
+            }
+        }
+    }
+
+    // The same for a stage whose rows 0..15 start at element offset off_lo
+    // and rows 16..31 at off_hi (consecutive rows D elements apart within a
+    // half): a stage of a paged K/V cache.  Rows >= nrows and halves whose
+    // page is invalid (ok_* false) are zero-filled and never read.
+    __device__ __forceinline__ void load_halves(const uint16_t* __restrict__ Kp,
+                                                const uint16_t* __restrict__ Vp, size_t off_lo,
+                                                size_t off_hi, bool ok_lo, bool ok_hi, int nrows,
+                                                int tid) {
+        static_assert(BC == 32, "two 16-row halves");
+#pragma unroll
+        for (int i = 0; i < kKIters; ++i) {
+            const int idx = tid + i * NT;
+            const bool in = (kKTotal % NT == 0) || idx < kKTotal;
+            const int row = idx / G::kChunks, c = idx % G::kChunks;
+            const bool hi = row >= 16;
+            const size_t off = (hi ? off_hi : off_lo) + (size_t)(row & 15) * D + c * 8;
+            k[i] = load16(Kp + off, in && row < nrows && (hi ? ok_hi : ok_lo));
+        }
+#pragma unroll
+        for (int i = 0; i < kVIters; ++i) {
+            const int idx = tid + i * NT;
+            const bool in = (kVTotal % NT == 0) || idx < kVTotal;
+            const int grp = idx % kVGroups, c = idx / kVGroups;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 4 * grp + r;
+                const bool hi = row >= 16;
+                const size_t off = (hi ? off_hi : off_lo) + (size_t)(row & 15) * D + c * 8;
+                v[i][r] = load16(Vp + off, in && row < nrows && (hi ? ok_hi : ok_lo));
             }
         }
     }
@@ -896,7 +937,37 @@ struct DecodeSmem {
     static constexpr int kBytes = kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes;
 };
 
+// Element offsets and validity of the two 16-row halves of a 32-row stage of
+// a paged K/V cache (page_size a power of two >= 16, stage start k0 a
+// multiple of 32, rows beyond kv_end not needed).
+struct PagedStage {
+    size_t lo, hi;
+    bool ok_lo, ok_hi;
+};
+
 template <int D>
+__device__ __forceinline__ PagedStage paged_stage(const AttnParams& p, int bseq, int hkv, int k0,
+                                                  int kv_end) {
+    PagedStage ps;
+    const int* tbl = p.block_table + (size_t)bseq * p.max_pages;
+    const int sh = p.page_shift;
+    const int pi = k0 >> sh;
+    const int id0 = tbl[pi];
+    ps.ok_lo = (unsigned)id0 < (unsigned)p.num_pages;
+    ps.lo = ((((size_t)(unsigned)id0 * p.heads_kv + hkv) << sh) + (size_t)(k0 & ((1 << sh) - 1))) * D;
+    if (sh == 4) {  // 16-row pages: the second half is the next page
+        const int id1 = k0 + 16 < kv_end ? tbl[pi + 1] : -1;
+        ps.ok_hi = (unsigned)id1 < (unsigned)p.num_pages;
+        ps.hi = (((size_t)(unsigned)id1 * p.heads_kv + hkv) << 4) * D;
+    } else {
+        ps.ok_hi = ps.ok_lo;
+        ps.hi = ps.lo + 16 * D;
+    }
+    return ps;
+}
+
+// kPaged: K / V are page pools addressed through p.block_table.
+template <int D, bool kPaged>
 __global__ __launch_bounds__(kDecodeThreads, DecodeCfg<D>::kWavesPerEU)
 void kf_attn_decode_kernel(AttnParams p) {
     using G = StageGeom<D, kDecodeStage>;
@@ -905,7 +976,7 @@ void kf_attn_decode_kernel(AttnParams p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
     const int split = blk % p.n_splits;
@@ -921,8 +992,9 @@ void kf_attn_decode_kernel(AttnParams p) {
     const int lim_min = p.causal ? max(kvb - p.q_len + 1, 0) : kvb;
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
-    const uint16_t* Kh = p.K + (size_t)grp * kv_len * D;
-    const uint16_t* Vh = p.V + (size_t)grp * kv_len * D;
+    const uint16_t* Kh = kPaged ? p.K : p.K + (size_t)grp * kv_len * D;
+    const uint16_t* Vh = kPaged ? p.V : p.V + (size_t)grp * kv_len * D;
+    const int bseq = grp / p.heads_kv, hkv = grp % p.heads_kv;  // paged addressing
 
     const int row = lane & 31;
     f16x8 qf[D / 16];
@@ -942,26 +1014,38 @@ void kf_attn_decode_kernel(AttnParams p) {
 
     StageLoader<D, kDecodeStage, 64> ld;
     int kv0 = s0 + wave * kDecodeStage;
-    if (kv0 < s1) ld.load(Kh, Vh, kv0, s1, lane);
+    PagedStage pc{0, 0, true, true}, pn{0, 0, true, true};
+    auto load_stage = [&](int k0, PagedStage& ps) {
+        if constexpr (kPaged) {
+            ps = paged_stage<D>(p, bseq, hkv, k0, s1);
+            ld.load_halves(Kh, Vh, ps.lo, ps.hi, ps.ok_lo, ps.ok_hi, s1 - k0, lane);
+        } else {
+            ld.load(Kh, Vh, k0, s1, lane);
+        }
+    };
+    if (kv0 < s1) load_stage(kv0, pc);
     while (kv0 < s1) {
         wave_lds_sync();  // previous stage's LDS reads are done
         ld.store(Ks, Vt, lane);
         wave_lds_sync();
         const int kv_next = kv0 + 4 * kDecodeStage;
-        if (kv_next < s1) ld.load(Kh, Vh, kv_next, s1, lane);
+        if (kv_next < s1) load_stage(kv_next, pn);
 
         f32x16 s[1];
         s[0] = qk_block<D, kDecodeStage>(Ks, 0, qf, lane);
-        if (kv0 + kDecodeStage > min(s1, lim_min)) {
+        if (kv0 + kDecodeStage > min(s1, lim_min) || !(pc.ok_lo && pc.ok_hi)) {
             const int lim = min(s1, lim_lane) - kv0;
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (acc_row(r, lane) >= lim) s[0][r] = -INFINITY;
+            for (int r = 0; r < 16; ++r) {
+                const int ar = acc_row(r, lane);
+                if (ar >= lim || !(ar < 16 ? pc.ok_lo : pc.ok_hi)) s[0][r] = -INFINITY;
+            }
         }
         f16x8 pb[2];
         softmax_update<1, G::kNTD>(s, st, o, p.scale_log2, pb);
         pv_accum<D, kDecodeStage, 2>(Vt, 0, pb, o, lane);
         kv0 = kv_next;
+        pc = pn;
     }
 
     // Rebase this wave's state onto its true max (natural-log scaled units).

@@ -179,7 +179,32 @@ def key_limits(q_len, kv_len, causal=False, kv_lens=None, B=1):
     return lim
 
 
-def sdpa(Q, K, V, acc=np.float64, causal=False, kv_lens=None):
+def paged_to_contiguous(K_pages, block_table, page_size):
+    """Gather a paged cache into per-sequence rows.
+
+    K_pages [num_pages, H_kv, page_size, D], block_table int [B, max_pages]
+    -> (K [B, H_kv, max_pages * page_size, D], key_valid bool [B, cap]):
+    key j of sequence b is row j % page_size of page block_table[b, j //
+    page_size] (the layout of reference_benchmarks/bench_flash_attn2.py:
+    153-215); keys on a page id outside [0, num_pages) are invalid (zeros).
+    """
+    num_pages, H_kv, ps, D = K_pages.shape
+    assert ps == page_size
+    table = np.asarray(block_table)
+    B, max_pages = table.shape
+    cap = max_pages * page_size
+    K = np.zeros((B, H_kv, cap, D), dtype=K_pages.dtype)
+    valid = np.zeros((B, cap), dtype=bool)
+    for b in range(B):
+        for pg in range(max_pages):
+            pid = int(table[b, pg])
+            if 0 <= pid < num_pages:
+                K[b, :, pg * page_size:(pg + 1) * page_size] = K_pages[pid]
+                valid[b, pg * page_size:(pg + 1) * page_size] = True
+    return K, valid
+
+
+def sdpa(Q, K, V, acc=np.float64, causal=False, kv_lens=None, key_valid=None):
     """Exact attention with GQA grouping; returns (O, Mi, Li).
 
     h_kv = h_q // (H_q // H_kv) (kernels/flash_attn.cu:406,
@@ -187,12 +212,13 @@ def sdpa(Q, K, V, acc=np.float64, causal=False, kv_lens=None):
     Li = sum_j exp(s - Mi); O = sum_j exp(s - Mi) v_j / Li.  Computed in
     ``acc`` precision (fp64 by default) from whatever values Q/K/V hold.
     With ``causal`` / ``kv_lens`` only the keys of key_limits() enter each
-    row; a row that sees none gets O = 0, Mi = -inf, Li = 0.
+    row, and with ``key_valid`` (bool [B, kv_len]) only valid keys; a row
+    that sees none gets O = 0, Mi = -inf, Li = 0.
     """
     B, H_q, H_kv, q_len, kv_len, D = _check_shapes(Q, K, V)
     ratio = H_q // H_kv
     scale = acc(1.0) / np.sqrt(acc(D))
-    masked = causal or kv_lens is not None
+    masked = causal or kv_lens is not None or key_valid is not None
     lim = key_limits(q_len, kv_len, causal, kv_lens, B) if masked else None
     O = np.empty((B, H_q, q_len, D), dtype=acc)
     M = np.empty((B, H_q, q_len), dtype=acc)
@@ -206,8 +232,10 @@ def sdpa(Q, K, V, acc=np.float64, causal=False, kv_lens=None):
             s = (q @ k.T) * scale
             if masked:
                 visible = np.arange(kv_len)[None, :] < lim[b][:, None]
+                if key_valid is not None:
+                    visible = visible & np.asarray(key_valid[b], dtype=bool)[None, :]
                 s = np.where(visible, s, -np.inf)
-                empty = lim[b] == 0
+                empty = ~visible.any(axis=1)
                 m = np.where(empty, 0.0, s.max(axis=1))
                 p = np.exp(s - m[:, None])
                 l = p.sum(axis=1)

@@ -195,3 +195,29 @@ def test_product_does_not_use_oracle():
                 text = open(os.path.join(root, fn)).read()
                 assert "import oracle" not in text and "from oracle" not in text, fn
                 assert "cpu_attn" not in text and "kf_oracle" not in text, fn
+
+
+def _paged(B=2, q=1, H_q=32, H_kv=8, D=128, ps=16, max_pages=64, num_pages=200, table=FAKE,
+           lens=FAKE, flags=0, ws=FAKE_WS, ws_bytes=1 << 30):
+    return kf.attn_decode_paged_ptr(FAKE, FAKE, FAKE, table, lens, FAKE, 0, 0, B, q, H_q, H_kv, D,
+                                    ps, max_pages, num_pages, flags, ws, ws_bytes)
+
+
+def test_paged_decode_validation():
+    for ps in (0, 8, 15, 24, 48, 3 << 10, 1 << 21):
+        assert _paged(ps=ps) == kf.KF_ERR_SIZE, ps
+    assert _paged(max_pages=0) == kf.KF_ERR_SIZE
+    assert _paged(num_pages=0) == kf.KF_ERR_SIZE
+    assert _paged(ps=1 << 20, max_pages=4096) == kf.KF_ERR_SIZE       # capacity beyond int
+    assert _paged(q=9, H_q=32, H_kv=8) == kf.KF_ERR_SIZE              # 36 rows per KV head
+    assert _paged(D=96) == kf.KF_ERR_HEAD_DIM
+    assert _paged(H_kv=3) == kf.KF_ERR_GQA
+    assert _paged(table=0) == kf.KF_ERR_NULL
+    assert _paged(lens=0) == kf.KF_ERR_NULL
+    assert _paged(table=FAKE + 2) == kf.KF_ERR_ALIGN
+    assert _paged(flags=4) == kf.KF_ERR_FLAGS
+    need = kf.paged_workspace_bytes(2, 1, 32, 8, 128, 16, 64)
+    assert need == kf.workspace_bytes(2, 1, 64 * 16, 32, 8, 128) > 0
+    assert _paged(ws_bytes=need - 1) == kf.KF_ERR_WORKSPACE
+    assert kf.paged_workspace_bytes(2, 9, 32, 8, 128, 16, 64) == 0    # not a decode shape
+    assert kf.paged_workspace_bytes(2, 1, 32, 8, 128, 24, 64) == 0    # bad page size

@@ -379,3 +379,55 @@ def test_planted_mask_off_by_one_is_caught(monkeypatch):
     Q, K, V = _rand((1, 2, 5, 16), 61), _rand((1, 2, 5, 16), 62), _rand((1, 2, 5, 16), 63)
     O, _, _ = orc.sdpa(Q, K, V, causal=True)
     assert not np.array_equal(O[:, :, 0], V[:, :, 0]), "off-by-one mask slipped through"
+
+
+# ---------------------------------------------------------------------------
+# Paged K/V cache: the gather restated two ways, and key validity.
+# ---------------------------------------------------------------------------
+def test_paged_gather_matches_reference_style_torch_gather():
+    """bench_flash_attn2.py:190-196 gathers with K_pool[blk_ids].permute(1, 0,
+    2, 3).reshape(H_kv, padded, D); per sequence that must equal the oracle."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    num_pages, H_kv, ps, D, B, max_pages = 12, 2, 16, 8, 2, 5
+    pool = rng.standard_normal((num_pages, H_kv, ps, D))
+    table = np.stack([rng.permutation(num_pages)[:max_pages] for _ in range(B)])
+    K, valid = orc.paged_to_contiguous(pool, table, ps)
+    assert valid.all()
+    for b in range(B):
+        ids = torch.from_numpy(table[b].astype(np.int64))
+        g = torch.from_numpy(pool)[ids].permute(1, 0, 2, 3).reshape(H_kv, max_pages * ps, D)
+        np.testing.assert_array_equal(K[b], g.numpy())
+
+
+def test_paged_identity_table_is_contiguous_and_invalid_ids_drop_keys():
+    rng = np.random.default_rng(6)
+    B, H_kv, max_pages, ps, D = 2, 2, 3, 16, 8
+    Kc = rng.standard_normal((B, H_kv, max_pages * ps, D))
+    # Pool page b * max_pages + p holds rows [p*ps, (p+1)*ps) of sequence b.
+    pool = Kc.reshape(B, H_kv, max_pages, ps, D).transpose(0, 2, 1, 3, 4).reshape(-1, H_kv, ps, D)
+    table = np.arange(B * max_pages).reshape(B, max_pages)
+    K, valid = orc.paged_to_contiguous(pool, table, ps)
+    np.testing.assert_array_equal(K, Kc)
+    table[1, 1] = -1
+    table[0, 2] = B * max_pages
+    _, valid = orc.paged_to_contiguous(pool, table, ps)
+    assert not valid[1, ps:2 * ps].any() and not valid[0, 2 * ps:].any()
+    assert valid.sum() == B * max_pages * ps - 2 * ps
+
+
+def test_sdpa_key_valid_equals_dropping_the_keys():
+    Q, K, V = _rand((2, 4, 3, 16), 71), _rand((2, 2, 20, 16), 72), _rand((2, 2, 20, 16), 73)
+    valid = np.ones((2, 20), dtype=bool)
+    valid[0, 5:9] = False
+    valid[1, :] = False
+    valid[1, 19] = True
+    O, M, L = orc.sdpa(Q, K, V, key_valid=valid)
+    keep = np.flatnonzero(valid[0])
+    O0, M0, L0 = orc.sdpa(Q[:1], K[:1, :, keep], V[:1, :, keep])
+    np.testing.assert_allclose(O[:1], O0, rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(M[:1], M0, rtol=1e-13)
+    # One valid key: O = that V row (closed form).
+    np.testing.assert_array_equal(O[1], np.repeat(V[1, :, 19:20], 2, axis=0).repeat(3, axis=1))
+    Oe, Me, Le = orc.sdpa(Q, K, V, key_valid=np.zeros((2, 20), dtype=bool))
+    assert (Oe == 0).all() and np.isneginf(Me).all() and (Le == 0).all()
