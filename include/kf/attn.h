@@ -26,7 +26,7 @@
  * kf_attn_fwd is non-causal with softmax scale 1/sqrt(D), as in the
  * reference; kf_attn_fwd_ex adds causal masking and per-sequence key
  * counts (ranked next steps of the reference's own roadmap,
- * docs/flash_attn.md:105 and tests/bench_flash_attn2.py:115-150).
+ * docs/flash_attn.md:105 and reference_benchmarks/bench_flash_attn2.py:115-150).
  * D must be one of the reference's instantiations
  * {16, 64, 128, 256} (flash_attn.cu:587-600).  All device pointers must be
  * 16-byte aligned.
@@ -54,8 +54,12 @@ enum kf_status {
     KF_ERR_FLAGS = 8       /* kf_attn_fwd_ex: unknown bits in `flags`            */
 };
 
-/* kf_attn_fwd_ex flags. */
+/* kf_attn_fwd_ex / kf_attn_decode_paged flags. */
 #define KF_ATTN_CAUSAL 1   /* query i sees keys j <= i + kv_b - q_len           */
+#define KF_ATTN_OUT_F16 2  /* O is written as fp16 (RNE of the fp32 result)     */
+#define KF_ATTN_OUT_BF16 4 /* O is written as bf16 (RNE of the fp32 result)     */
+#define KF_ATTN_LSE 8      /* row_max receives LSE = Mi + ln(Li) (natural log;
+                              -inf for a row without keys); row_sumexp unused */
 
 /* Which kernels kf_attn_fwd runs for a shape (see kf_attn_plan). */
 enum kf_path {
@@ -115,10 +119,15 @@ int kf_attn_fwd(const void* Q, const void* K, const void* V, float* O,
  *   corner (the last query sees every key; with q_len == kv_len it is the
  *   usual lower triangle; q_len = 1 decode is unaffected).
  * A query row that sees no key (kv_b = 0, or causal rows with
- * i + kv_b - q_len < 0) gets O = 0, Mi = -inf, Li = 0.  Shapes, workspace
+ * i + kv_b - q_len < 0) gets O = 0, Mi = -inf, Li = 0.
+ * O is fp32 [B, H_q, q_len, D] unless flags select KF_ATTN_OUT_F16 or
+ * KF_ATTN_OUT_BF16 (then 2-byte elements, still 16-byte aligned; the
+ * reference's PyTorch comparator outputs fp16, bench_flash_attn2.py:11-12);
+ * KF_ATTN_LSE replaces the (Mi, Li) pair by one log-sum-exp per row in
+ * row_max.  KF_ATTN_OUT_F16 | KF_ATTN_OUT_BF16 -> KF_ERR_FLAGS.  Shapes, workspace
  * and the kernels chosen are those of kf_attn_fwd (kf_attn_plan,
  * kf_attn_workspace_bytes apply unchanged). */
-int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, float* O,
+int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, void* O,
                    float* row_max, float* row_sumexp,
                    int B, int q_len, int kv_len, int H_q, int H_kv, int D,
                    const int* kv_lens, int flags,
@@ -148,7 +157,7 @@ size_t kf_attn_decode_paged_workspace_bytes(int B, int q_len, int H_q, int H_kv,
                                             int page_size, int max_pages_per_seq);
 int kf_attn_decode_paged(const void* Q, const void* K_pages, const void* V_pages,
                          const int* block_table, const int* kv_lens,
-                         float* O, float* row_max, float* row_sumexp,
+                         void* O, float* row_max, float* row_sumexp,
                          int B, int q_len, int H_q, int H_kv, int D,
                          int page_size, int max_pages_per_seq, int num_pages, int flags,
                          void* workspace, size_t workspace_bytes, void* stream);

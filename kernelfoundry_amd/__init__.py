@@ -35,6 +35,7 @@ __all__ = [
     "attn_fwd_ptr", "launch_flash_attn", "status_string", "exported_symbols",
     "KF_OK", "KF_ERR_HEAD_DIM", "KF_ERR_GQA", "KF_ERR_SIZE", "KF_ERR_NULL",
     "KF_ERR_WORKSPACE", "KF_ERR_ALIGN", "KF_ERR_HIP", "KF_ERR_FLAGS", "KF_ATTN_CAUSAL",
+    "KF_ATTN_OUT_F16", "KF_ATTN_OUT_BF16", "KF_ATTN_LSE",
     "PATH_NAMES", "attn_fwd_ex_ptr", "attn_decode_paged", "attn_decode_paged_ptr",
     "paged_workspace_bytes",
 ]
@@ -53,6 +54,9 @@ KF_ERR_ALIGN = 6
 KF_ERR_HIP = 7
 KF_ERR_FLAGS = 8
 KF_ATTN_CAUSAL = 1
+KF_ATTN_OUT_F16 = 2
+KF_ATTN_OUT_BF16 = 4
+KF_ATTN_LSE = 8
 
 PATH_NAMES = {0: "prefill", 1: "decode", 2: "decode_split"}
 
@@ -186,16 +190,29 @@ def launch_flash_attn(Q, K, V, O, B, S, H_q, H_kv, D, stream=0) -> int:
     return int(load_library().kf_launch_flash_attn(Q, K, V, O, B, S, H_q, H_kv, D, stream or None))
 
 
+def _out_flags(torch, out_dtype, return_lse):
+    f = {None: 0, torch.float32: 0, torch.float16: KF_ATTN_OUT_F16,
+         torch.bfloat16: KF_ATTN_OUT_BF16}
+    if out_dtype not in f:
+        raise ValueError("out_dtype must be float32, float16 or bfloat16")
+    return f[out_dtype] | (KF_ATTN_LSE if return_lse else 0)
+
+
 def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=None,
-             causal=False, kv_lens=None):
+             causal=False, kv_lens=None, out_dtype=None, return_lse=False):
     """Attention forward on torch tensors resident on the GPU.
 
     Q [B, H_q, q_len, D] fp16, K/V [B, H_kv, kv_len, D] fp16, contiguous.
-    Returns O [B, H_q, q_len, D] fp32, or (O, Mi, Li) with ``return_stats``.
+    Returns O [B, H_q, q_len, D] (fp32, or ``out_dtype`` fp16 / bf16), or
+    (O, Mi, Li) with ``return_stats``, or (O, LSE) with ``return_lse``.
     Asynchronous on ``stream`` (default: torch's current stream).
     ``causal`` / ``kv_lens`` (int32 GPU tensor [B]) select kf_attn_fwd_ex.
     """
     import torch
+
+    if return_stats and return_lse:
+        raise ValueError("return_stats and return_lse are exclusive")
+    flags = _out_flags(torch, out_dtype, return_lse)
 
     if Q.dtype != torch.float16 or K.dtype != torch.float16 or V.dtype != torch.float16:
         raise TypeError("Q, K, V must be float16")
@@ -210,10 +227,11 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
     if Bk != B or Dk != D:
         raise ValueError("Q and K/V disagree on B or D")
     if out is None:
-        out = torch.empty((B, H_q, q_len, D), dtype=torch.float32, device=Q.device)
+        out = torch.empty((B, H_q, q_len, D), dtype=out_dtype or torch.float32, device=Q.device)
     Mi = Li = None
-    if return_stats:
+    if return_stats or return_lse:
         Mi = torch.empty((B, H_q, q_len), dtype=torch.float32, device=Q.device)
+    if return_stats:
         Li = torch.empty_like(Mi)
     need = workspace_bytes(B, q_len, kv_len, H_q, H_kv, D)
     if stream is None:
@@ -230,7 +248,7 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
                          Li.data_ptr() if Li is not None else 0,
                          B, q_len, kv_len, H_q, H_kv, D,
                          kv_lens.data_ptr() if kv_lens is not None else 0,
-                         KF_ATTN_CAUSAL if causal else 0,
+                         (KF_ATTN_CAUSAL if causal else 0) | flags,
                          workspace.data_ptr() if (need and workspace is not None) else 0,
                          need, stream.cuda_stream)
     if st != KF_OK:
@@ -238,11 +256,14 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
         if st == KF_ERR_HIP:
             msg += f" (hipError_t {load_library().kf_last_hip_error()})"
         raise KfError(st, msg)
+    if return_lse:
+        return out, Mi
     return (out, Mi, Li) if return_stats else out
 
 
 def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, return_stats=False,
-                      causal=False, workspace=None, stream=None):
+                      causal=False, workspace=None, stream=None, out_dtype=None,
+                      return_lse=False):
     """Decode over a paged K/V cache on torch GPU tensors.
 
     Q [B, H_q, q_len, D] fp16; K_pages / V_pages [num_pages, H_kv, page_size,
@@ -251,6 +272,9 @@ def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, re
     """
     import torch
 
+    if return_stats and return_lse:
+        raise ValueError("return_stats and return_lse are exclusive")
+    flags = _out_flags(torch, out_dtype, return_lse)
     for t, name in ((Q, "Q"), (K_pages, "K_pages"), (V_pages, "V_pages")):
         if t.dtype != torch.float16 or not t.is_cuda or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous float16 GPU tensor")
@@ -265,10 +289,11 @@ def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, re
         raise ValueError("block_table must be [B, max_pages_per_seq] and kv_lens [B]")
     max_pages = block_table.shape[1]
     if out is None:
-        out = torch.empty((B, H_q, q_len, D), dtype=torch.float32, device=Q.device)
+        out = torch.empty((B, H_q, q_len, D), dtype=out_dtype or torch.float32, device=Q.device)
     Mi = Li = None
-    if return_stats:
+    if return_stats or return_lse:
         Mi = torch.empty((B, H_q, q_len), dtype=torch.float32, device=Q.device)
+    if return_stats:
         Li = torch.empty_like(Mi)
     need = paged_workspace_bytes(B, q_len, H_q, H_kv, D, page_size, max_pages)
     if stream is None:
@@ -281,7 +306,7 @@ def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, re
                                Mi.data_ptr() if Mi is not None else 0,
                                Li.data_ptr() if Li is not None else 0,
                                B, q_len, H_q, H_kv, D, page_size, max_pages, num_pages,
-                               KF_ATTN_CAUSAL if causal else 0,
+                               (KF_ATTN_CAUSAL if causal else 0) | flags,
                                workspace.data_ptr() if (need and workspace is not None) else 0,
                                need, stream.cuda_stream)
     if st != KF_OK:
@@ -289,4 +314,6 @@ def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, re
         if st == KF_ERR_HIP:
             msg += f" (hipError_t {load_library().kf_last_hip_error()})"
         raise KfError(st, msg)
+    if return_lse:
+        return out, Mi
     return (out, Mi, Li) if return_stats else out

@@ -124,10 +124,12 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
 // Shared tail of kf_attn_fwd_ex and kf_attn_decode_paged: pointer and
 // workspace checks, the common kernel parameters, the launches.  `prm`
 // arrives with the masking / paging fields already set.
-int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const void* V, float* O,
+int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const void* V, void* O,
         float* row_max, float* row_sumexp, int q_len, int kv_len, int H_kv, int D, int flags,
         void* workspace, size_t workspace_bytes, void* stream) {
-    if ((flags & ~KF_ATTN_CAUSAL) != 0) return KF_ERR_FLAGS;
+    constexpr int kKnown = KF_ATTN_CAUSAL | KF_ATTN_OUT_F16 | KF_ATTN_OUT_BF16 | KF_ATTN_LSE;
+    if ((flags & ~kKnown) != 0) return KF_ERR_FLAGS;
+    if ((flags & KF_ATTN_OUT_F16) && (flags & KF_ATTN_OUT_BF16)) return KF_ERR_FLAGS;
     if (!Q || !K || !V || !O) return KF_ERR_NULL;
     if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O)) return KF_ERR_ALIGN;
     if ((reinterpret_cast<uintptr_t>(prm.kv_lens) & 3u) != 0) return KF_ERR_ALIGN;
@@ -140,7 +142,9 @@ int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const 
     prm.Q = static_cast<const uint16_t*>(Q);
     prm.K = static_cast<const uint16_t*>(K);
     prm.V = static_cast<const uint16_t*>(V);
-    prm.O = O;
+    prm.O = static_cast<float*>(O);
+    prm.out_dtype = (flags & KF_ATTN_OUT_F16) ? kf::kOutF16 : (flags & KF_ATTN_OUT_BF16) ? kf::kOutBF16 : kf::kOutF32;
+    prm.lse = (flags & KF_ATTN_LSE) ? 1 : 0;
     prm.Mi = row_max;
     prm.Li = row_sumexp;
     if (pl.ws_bytes > 0) {
@@ -222,7 +226,7 @@ int kf_attn_fwd(const void* Q, const void* K, const void* V, float* O, float* ro
                           nullptr, 0, workspace, workspace_bytes, stream);
 }
 
-int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, float* O, float* row_max,
+int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, void* O, float* row_max,
                    float* row_sumexp, int B, int q_len, int kv_len, int H_q, int H_kv, int D,
                    const int* kv_lens, int flags, void* workspace, size_t workspace_bytes,
                    void* stream) {
@@ -246,7 +250,7 @@ size_t kf_attn_decode_paged_workspace_bytes(int B, int q_len, int H_q, int H_kv,
 }
 
 int kf_attn_decode_paged(const void* Q, const void* K_pages, const void* V_pages,
-                         const int* block_table, const int* kv_lens, float* O, float* row_max,
+                         const int* block_table, const int* kv_lens, void* O, float* row_max,
                          float* row_sumexp, int B, int q_len, int H_q, int H_kv, int D,
                          int page_size, int max_pages_per_seq, int num_pages, int flags,
                          void* workspace, size_t workspace_bytes, void* stream) {

@@ -103,7 +103,46 @@ struct AttnParams {
     int max_pages;      // block_table row length; kv_len = max_pages * page_size
     int page_shift;     // log2(page_size), page_size >= 16
     int num_pages;
+    // Output format: O elements fp32 / fp16 / bf16 (kOut*); with `lse` the
+    // Mi slot receives LSE = Mi + ln(Li) and Li is not written.
+    int out_dtype;
+    int lse;
 };
+
+enum : int { kOutF32 = 0, kOutF16 = 1, kOutBF16 = 2 };
+
+// fp32 -> bf16 bits, round to nearest even (inputs are finite).
+__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Store the 4 consecutive output elements O[e .. e+3] in p.out_dtype
+// (e is a multiple of 4; O is 16-byte aligned).
+__device__ __forceinline__ void store_out4(const AttnParams& p, size_t e, const f32x4& v) {
+    if (p.out_dtype == kOutF32) {
+        *reinterpret_cast<f32x4*>(p.O + e) = v;
+    } else if (p.out_dtype == kOutF16) {
+        const f16x4 h = __builtin_convertvector(v, f16x4);
+        *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(p.O) + e) = h;
+    } else {
+        u32x2 w;
+        w.x = bf16_rne_bits(v[0]) | (bf16_rne_bits(v[1]) << 16);
+        w.y = bf16_rne_bits(v[2]) | (bf16_rne_bits(v[3]) << 16);
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.O) + e) = w;
+    }
+}
+
+// Row statistics of query row r: Mi and Li, or LSE = Mi + ln(Li) (-inf for a
+// row without keys) into the Mi slot.
+__device__ __forceinline__ void store_stats(const AttnParams& p, size_t r, float mi, float li) {
+    if (p.lse) {
+        if (p.Mi) p.Mi[r] = li > 0.f ? mi + __logf(li) : -INFINITY;
+    } else {
+        if (p.Mi) p.Mi[r] = mi;
+        if (p.Li) p.Li[r] = li;
+    }
+}
 
 // Keys of the sequence that KV-head group `grp` belongs to, clamped to
 // [0, kv_len].
@@ -762,19 +801,15 @@ void kf_attn_prefill_kernel(AttnParams p) {
     if (kMask && ntiles == 0) {
         // No key for any row of this workgroup (whole-workgroup uniform).
         if (row < R) {
-            float* Orow = p.O + ((size_t)grp * R + row) * D;
+            const size_t ri = (size_t)grp * R + row;
 #pragma unroll
             for (int td = 0; td < kNTD; ++td)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int d = 32 * td + 8 * i + 4 * g;
-                    if (d < D) *reinterpret_cast<f32x4*>(Orow + d) = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (d < D) store_out4(p, ri * D + d, f32x4{0.f, 0.f, 0.f, 0.f});
                 }
-            if (g == 0) {
-                const size_t ri = (size_t)grp * R + row;
-                if (p.Mi) p.Mi[ri] = -INFINITY;
-                if (p.Li) p.Li[ri] = 0.f;
-            }
+            if (g == 0) store_stats(p, ri, -INFINITY, 0.f);
         }
         return;
     }
@@ -896,7 +931,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const bool empty = kMask && !(l > 0.f);  // no visible key
     if (row < R) {
         const float inv = empty ? 0.f : 1.0f / l;
-        float* Orow = p.O + ((size_t)grp * R + row) * D;
+        const size_t ri = (size_t)grp * R + row;
 #pragma unroll
         for (int td = 0; td < kNTD; ++td)
 #pragma unroll
@@ -905,14 +940,12 @@ void kf_attn_prefill_kernel(AttnParams p) {
                 if (d < D) {
                     f32x4 v = {o[td][4 * i] * inv, o[td][4 * i + 1] * inv,
                                o[td][4 * i + 2] * inv, o[td][4 * i + 3] * inv};
-                    *reinterpret_cast<f32x4*>(Orow + d) = v;
+                    store_out4(p, ri * D + d, v);
                 }
             }
-        if (g == 0) {
-            const size_t ri = (size_t)grp * R + row;
-            if (p.Mi) p.Mi[ri] = st.rmax * p.scale;
-            if (p.Li) p.Li[ri] = empty ? 0.f : l * exp2_hw(st.m - st.rmax * p.scale_log2);
-        }
+        if (g == 0)
+            store_stats(p, ri, st.rmax * p.scale,
+                        empty ? 0.f : l * exp2_hw(st.m - st.rmax * p.scale_log2));
     }
 }
 
@@ -1095,10 +1128,9 @@ void kf_attn_decode_kernel(AttnParams p) {
         }
         const bool final_out = p.n_splits == 1;
         const float inv = final_out ? (l > 0.f ? 1.0f / l : 0.f) : 1.0f;
-        // Final rows go to O; split partials to [grp][split][row][D].
+        // Final rows go to O; split partials (fp32) to [grp][split][row][D].
         const size_t ri = (size_t)grp * R + mrow;
         const size_t pi = ((size_t)grp * p.n_splits + split) * R + mrow;
-        float* dst = final_out ? p.O + ri * D : p.Opart + pi * D;
 #pragma unroll
         for (int j = 0; j < kSeg; j += 4) {
             const int d = seg * kSeg + j;
@@ -1108,12 +1140,14 @@ void kf_attn_decode_kernel(AttnParams p) {
                 const f32x4 v = *reinterpret_cast<const f32x4*>(Ob + (w * 32 + mrow) * SM::kOStride + d);
                 acc += wt[w] * v;
             }
-            *reinterpret_cast<f32x4*>(dst + d) = acc * inv;
+            if (final_out)
+                store_out4(p, ri * D + d, acc * inv);
+            else
+                *reinterpret_cast<f32x4*>(p.Opart + pi * D + d) = acc;
         }
         if (seg == 0) {
             if (final_out) {
-                if (p.Mi) p.Mi[ri] = m;
-                if (p.Li) p.Li[ri] = l;
+                store_stats(p, ri, m, l);
             } else {
                 p.Mpart[pi] = m;
                 p.Lpart[pi] = l;
@@ -1196,11 +1230,8 @@ void kf_attn_split_merge_kernel(AttnParams p) {
         f32x4 t = s_acc[0][tid];
 #pragma unroll
         for (int j = 1; j < kLanes; ++j) t += s_acc[j][tid];
-        *reinterpret_cast<f32x4*>(p.O + (size_t)row * D + 4 * tid) = t * (l > 0.f ? 1.0f / l : 0.f);
-        if (tid == 0) {
-            if (p.Mi) p.Mi[row] = m;
-            if (p.Li) p.Li[row] = l;
-        }
+        store_out4(p, (size_t)row * D + 4 * tid, t * (l > 0.f ? 1.0f / l : 0.f));
+        if (tid == 0) store_stats(p, row, m, l);
     }
 }
 

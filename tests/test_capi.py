@@ -104,8 +104,9 @@ def _fwd_ex(kv_lens=0, flags=0, **kw):
 
 
 def test_fwd_ex_validation():
-    assert _fwd_ex(flags=2) == kf.KF_ERR_FLAGS
+    assert _fwd_ex(flags=16) == kf.KF_ERR_FLAGS
     assert _fwd_ex(flags=-1) == kf.KF_ERR_FLAGS
+    assert _fwd_ex(flags=kf.KF_ATTN_OUT_F16 | kf.KF_ATTN_OUT_BF16) == kf.KF_ERR_FLAGS
     assert _fwd_ex(kv_lens=FAKE + 2) == kf.KF_ERR_ALIGN        # int array: 4-byte aligned
     assert _fwd_ex(D=96, flags=kf.KF_ATTN_CAUSAL) == kf.KF_ERR_HEAD_DIM
     assert _fwd_ex(H_kv=3, flags=kf.KF_ATTN_CAUSAL) == kf.KF_ERR_GQA
@@ -215,7 +216,8 @@ def test_paged_decode_validation():
     assert _paged(table=0) == kf.KF_ERR_NULL
     assert _paged(lens=0) == kf.KF_ERR_NULL
     assert _paged(table=FAKE + 2) == kf.KF_ERR_ALIGN
-    assert _paged(flags=4) == kf.KF_ERR_FLAGS
+    assert _paged(flags=16) == kf.KF_ERR_FLAGS
+    assert _paged(flags=kf.KF_ATTN_OUT_F16 | kf.KF_ATTN_OUT_BF16) == kf.KF_ERR_FLAGS
     need = kf.paged_workspace_bytes(2, 1, 32, 8, 128, 16, 64)
     assert need == kf.workspace_bytes(2, 1, 64 * 16, 32, 8, 128) > 0
     assert _paged(ws_bytes=need - 1) == kf.KF_ERR_WORKSPACE

@@ -1,0 +1,104 @@
+"""GPU checks of the output formats of kf_attn_fwd_ex / kf_attn_decode_paged:
+fp16 and bf16 O, and the LSE row statistic.
+
+The kernels compute O in fp32 and round only at the store, so an fp16 / bf16
+O must equal the round-to-nearest-even of the fp32 O of the same call
+configuration bit for bit (numpy's float16 cast and an explicit bf16 RNE on
+the bits are the references).  LSE must equal Mi + ln(Li) of the fp32 call
+(to the accuracy of the hardware log) and the fp64 oracle's
+Mi + ln(Li) to 1e-3; rows without keys give LSE = -inf.
+
+Every kernel path that writes O is covered: prefill (unmasked and masked),
+decode without split (O written by the decode kernel), decode with split
+(O written by the merge kernel), and paged decode.
+"""
+import numpy as np
+import pytest
+
+from oracle import attn_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    return torch
+
+
+def _announce(**kw):
+    print("case", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _bf16_rne(x32):
+    u = np.ascontiguousarray(x32, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+CASES = [
+    # B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens       path
+    (1, 8, 2, 300, 300, 128, False, None),                # prefill
+    (2, 8, 2, 200, 260, 64, True, [260, 0]),              # prefill, masked, empty sequence
+    (1, 4, 4, 64, 64, 256, False, None),                  # prefill D=256
+    (2, 8, 8, 1, 100, 16, False, None),                   # decode, one split
+    (2, 32, 8, 1, 3000, 128, True, [3000, 7]),            # decode + merge kernel
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_q{}_kv{}_D{}".format(*c[:6]))
+def test_output_formats_round_the_fp32_result(case):
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens = case
+    _announce(test="out_formats", B=B, H_q=H_q, H_kv=H_kv, q_len=q_len, kv_len=kv_len, D=D,
+              causal=causal, kv_lens=kv_lens)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, q_len, kv_len, D, 555 + D)
+    Q, K, V = (torch.from_numpy(x).cuda() for x in (q16, k16, v16))
+    lens = None if kv_lens is None else torch.tensor(kv_lens, dtype=torch.int32, device="cuda")
+    kw = dict(causal=causal, kv_lens=lens)
+    O32, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True, **kw)
+    O16 = kf.attn_fwd(Q, K, V, out_dtype=torch.float16, **kw)
+    Obf, lse = kf.attn_fwd(Q, K, V, out_dtype=torch.bfloat16, return_lse=True, **kw)
+    torch.cuda.synchronize()
+    O32 = O32.cpu().numpy()
+    assert O16.dtype == torch.float16 and Obf.dtype == torch.bfloat16
+    np.testing.assert_array_equal(O16.cpu().numpy().view(np.uint16),
+                                  O32.astype(np.float16).view(np.uint16))
+    np.testing.assert_array_equal(Obf.cpu().view(torch.int16).numpy().view(np.uint16),
+                                  _bf16_rne(O32))
+    Mi, Li, lse = Mi.cpu().numpy(), Li.cpu().numpy(), lse.cpu().numpy()
+    empty = Li == 0
+    assert np.isneginf(lse[empty]).all()
+    full = ~empty
+    np.testing.assert_allclose(lse[full], Mi[full] + np.log(Li[full]), rtol=0, atol=1e-5)
+    _, Mr, Lr = orc.sdpa(q16, k16, v16, causal=causal, kv_lens=kv_lens)
+    ref = Mr + np.log(np.where(Lr > 0, Lr, 1.0))
+    assert np.abs(lse[full] - ref[full]).max() <= 1e-3
+
+
+def test_paged_output_formats():
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    B, H_q, H_kv, D, ps, max_pages = 2, 32, 8, 128, 16, 40
+    num_pages = B * max_pages
+    _announce(test="paged_out_formats")
+    rng = np.random.default_rng(77)
+    f16 = lambda a: a.astype(np.float32).astype(np.float16)
+    q16 = f16(rng.standard_normal((B, H_q, 1, D)))
+    kp = f16(rng.standard_normal((num_pages, H_kv, ps, D)))
+    vp = f16(rng.standard_normal((num_pages, H_kv, ps, D)))
+    table = rng.permutation(num_pages).astype(np.int32).reshape(B, max_pages)
+    lens = np.array([600, 17], dtype=np.int32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    args = (t(q16), t(kp), t(vp), t(table), t(lens))
+    O32, Mi, Li = kf.attn_decode_paged(*args, return_stats=True)
+    O16, lse = kf.attn_decode_paged(*args, out_dtype=torch.float16, return_lse=True)
+    Obf = kf.attn_decode_paged(*args, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    O32 = O32.cpu().numpy()
+    np.testing.assert_array_equal(O16.cpu().numpy().view(np.uint16),
+                                  O32.astype(np.float16).view(np.uint16))
+    np.testing.assert_array_equal(Obf.cpu().view(torch.int16).numpy().view(np.uint16),
+                                  _bf16_rne(O32))
+    np.testing.assert_allclose(lse.cpu().numpy(), Mi.cpu().numpy() + np.log(Li.cpu().numpy()),
+                               rtol=0, atol=1e-5)
