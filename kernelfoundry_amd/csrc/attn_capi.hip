@@ -38,6 +38,7 @@ struct Plan {
     int row_tiles;
     int grid;
     int threads;
+    int waves;          // prefill: waves per workgroup
     size_t ws_bytes;
     size_t ws_o_off, ws_m_off, ws_l_off;
 };
@@ -74,14 +75,21 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) 
         p.threads = kf::kDecodeThreads;
         p.path = splits > 1 ? KF_PATH_DECODE_SPLIT : KF_PATH_DECODE;
     } else {
-        const int rows = kf::prefill_rows_per_block(D);
+        // Waves per workgroup: the most the head dimension allows, halved
+        // (down to 2) while the grid would leave CUs without a workgroup.
+        // D = 256 stays at 4 waves (its accumulators need a SIMD per wave).
+        int nw = kf::prefill_max_waves(D);
+        const int nw_min = D >= 256 ? 4 : 2;
+        while (nw > nw_min && n_groups * ((R + 32 * nw - 1) / (32 * nw)) < kNumCUs) nw /= 2;
+        const int rows = 32 * nw;
         const long long row_tiles = (R + rows - 1) / rows;
         if (n_groups * row_tiles > INT_MAX) return KF_ERR_SIZE;
         p.n_splits = 1;
         p.kv_per_split = kv_len;
         p.row_tiles = (int)row_tiles;
         p.grid = (int)(n_groups * row_tiles);
-        p.threads = kf::prefill_threads(D);
+        p.threads = 64 * nw;
+        p.waves = nw;
         p.path = KF_PATH_PREFILL;
     }
     if (p.path == KF_PATH_DECODE_SPLIT) {
@@ -102,13 +110,28 @@ int hip_fail(hipError_t e) {
     return KF_ERR_HIP;
 }
 
+template <int D, int NW>
+void launch_prefill(const Plan& pl, const kf::AttnParams& prm, bool mask, hipStream_t stream) {
+    if (mask)
+        kf::kf_attn_prefill_kernel<D, true, NW><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+    else
+        kf::kf_attn_prefill_kernel<D, false, NW><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+}
+
 template <int D>
 hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t stream) {
     if (pl.path == KF_PATH_PREFILL) {
-        if (prm.causal || prm.kv_lens)
-            kf::kf_attn_prefill_kernel<D, true><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
-        else
-            kf::kf_attn_prefill_kernel<D, false><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+        const bool mask = prm.causal || prm.kv_lens;
+        if constexpr (D >= 256) {
+            launch_prefill<D, 4>(pl, prm, mask, stream);
+        } else {
+            if (pl.waves == 8)
+                launch_prefill<D, 8>(pl, prm, mask, stream);
+            else if (pl.waves == 4)
+                launch_prefill<D, 4>(pl, prm, mask, stream);
+            else
+                launch_prefill<D, 2>(pl, prm, mask, stream);
+        }
         return hipGetLastError();
     }
     if (prm.block_table)

@@ -484,26 +484,37 @@ template <> struct SwizzleRow<256> : SwizzleRow<128> {};
 // Per head dimension: waves per workgroup (32 query rows each) and whether
 // S(t+1) = K Q^T is overlapped with the softmax of tile t (that needs a second
 // score block in registers).  D = 256 holds 128 fp32 O accumulators per lane,
-// so it runs 4 waves (one per SIMD, up to 512 registers) without the overlap.
-template <int D> struct PrefillCfg {
+// so it runs at most 4 waves (one per SIMD, up to 512 registers) without the
+// overlap.  Grids too small to give every CU a workgroup use fewer waves per
+// workgroup (NW = 4 or 2) so that more CUs take part.
+template <int D> constexpr int kPrefillMaxWaves = D >= 256 ? 4 : 8;
+
+constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
+
+template <int D, int NW = kPrefillMaxWaves<D>> struct PrefillCfg {
     static constexpr int BC = 32;                   // KV rows per MFMA tile
-    static constexpr int kWaves = D >= 256 ? 4 : 8;
+    static constexpr int kWaves = NW;
     static constexpr int kThreads = 64 * kWaves;
     static constexpr int kRows = 32 * kWaves;
-    static constexpr int kWavesPerEU = kWaves / 4;
+    // Register budget: 256 per wave (two waves per SIMD) for D <= 128,
+    // whatever the workgroup size, so every variant keeps its accumulators in
+    // VGPRs; 512 for D = 256.
+    static constexpr int kWavesPerEU = D >= 256 ? 1 : 2;
     static constexpr bool kPipeline = D <= 128;
     // Pipelined: stages t, t+1 and the one being filled rotate through three
     // LDS buffers; otherwise two suffice (and keep every LDS offset of D = 256
     // inside the 16-bit instruction offset field).
     static constexpr int kBuffers = kPipeline ? 3 : 2;
-    // Tiles per LDS stage.  Pipelined, one stage holds two tiles, so the
-    // workgroup barrier and the LDS-DMA issue come once per 64 kv rows.
-    static constexpr int kSub = kPipeline ? 2 : 1;
+    // Tiles per LDS stage.  Pipelined 8-wave workgroups hold two tiles per
+    // stage, so the workgroup barrier and the LDS-DMA issue come once per 64
+    // kv rows.  Smaller workgroups keep one tile per stage: their LDS (48 KB
+    // at D = 128) then admits two waves per SIMD, which holds the compiler to
+    // the 256-register budget.
+    static constexpr int kSub = (kPipeline && kWaves >= 8) ? 2 : 1;
     static constexpr int kStageRows = BC * kSub;
 };
 
-inline int prefill_rows_per_block(int D) { return D >= 256 ? PrefillCfg<256>::kRows : PrefillCfg<128>::kRows; }
-inline int prefill_threads(int D) { return D >= 256 ? PrefillCfg<256>::kThreads : PrefillCfg<128>::kThreads; }
+inline int prefill_max_waves(int D) { return D >= 256 ? kPrefillMaxWaves<256> : kPrefillMaxWaves<128>; }
 
 template <int D, int BC, int NW>
 struct DmaStage {
@@ -595,20 +606,21 @@ __device__ __forceinline__ void block_update_max(RowState& st, float mx, float s
 
 // kMask: causal masking and/or per-sequence key counts (p.causal,
 // p.kv_lens); without it every row sees keys [0, kv_len).
-template <int D, bool kMask>
-__global__ __launch_bounds__(PrefillCfg<D>::kThreads, PrefillCfg<D>::kWavesPerEU)
+template <int D, bool kMask, int NW = kPrefillMaxWaves<D>>
+__global__ __launch_bounds__((PrefillCfg<D, NW>::kThreads), (PrefillCfg<D, NW>::kWavesPerEU))
 void kf_attn_prefill_kernel(AttnParams p) {
-    constexpr int BC = PrefillCfg<D>::BC;
+    using Cfg = PrefillCfg<D, NW>;
+    constexpr int BC = Cfg::BC;
     constexpr int kNSB = BC / 32;                 // 32-row score blocks per stage
-    constexpr int kPrefillWaves = PrefillCfg<D>::kWaves;
-    constexpr int kPrefillRows = PrefillCfg<D>::kRows;
-    constexpr int kSub = PrefillCfg<D>::kSub;      // tiles per LDS stage
-    constexpr int SR = PrefillCfg<D>::kStageRows;  // kv rows per LDS stage
+    constexpr int kPrefillWaves = Cfg::kWaves;
+    constexpr int kPrefillRows = Cfg::kRows;
+    constexpr int kSub = Cfg::kSub;               // tiles per LDS stage
+    constexpr int SR = Cfg::kStageRows;           // kv rows per LDS stage
     using S = DmaStage<D, SR, kPrefillWaves>;
     using SW = SwizzleRow<D>;
     constexpr int kNKK = D / 16;                  // MFMA k-steps over D
     constexpr int kNTD = (D < 32 ? 32 : D) / 32;  // 32-row O^T tiles
-    constexpr bool kPipe = PrefillCfg<D>::kPipeline;
+    constexpr bool kPipe = Cfg::kPipeline;
     __shared__ __attribute__((aligned(1024))) char buf0[S::kStageBytes];
     __shared__ __attribute__((aligned(1024))) char buf1[S::kStageBytes];
     __shared__ __attribute__((aligned(1024))) char buf2[kPipe ? S::kStageBytes : 16];
@@ -672,11 +684,15 @@ void kf_attn_prefill_kernel(AttnParams p) {
     // ii = (j mod kInstrPerTensor) of the K (j < kInstrPerTensor) or V region,
     // i.e. row r = ii * kRowsPerInstr + l / kChunks, physical chunk
     // l % kChunks, which holds logical chunk (l % kChunks) ^ h(r) of kv row r.
-    // lane_base[i]: byte offset of lane l's source chunk relative to the
-    // first row of instruction i (identical for all i unless D = 256).
-    uint32_t lane_base[S::kPerWave];
+    // lane_base[i % kLBPeriod]: byte offset of lane l's source chunk
+    // relative to the first row of instruction i.  The swizzle depends on
+    // row & 15 only, so instruction i repeats the offsets of instruction
+    // i - kLBPeriod: kLaneBases distinct row phases, visited with stride W.
+    constexpr int kLaneBases = S::kRowsPerInstr >= 16 ? 1 : 16 / S::kRowsPerInstr;
+    constexpr int kLBPeriod = kLaneBases / gcd_int(kPrefillWaves, kLaneBases);
+    uint32_t lane_base[kLBPeriod];
 #pragma unroll
-    for (int i = 0; i < S::kPerWave; ++i) {
+    for (int i = 0; i < kLBPeriod; ++i) {
         const int ii = (wave + kPrefillWaves * i) % S::kInstrPerTensor;
         const int lr = lane / S::kChunks;
         const int r = ii * S::kRowsPerInstr + lr;
@@ -698,7 +714,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
                     char* d = dst + (is_v ? S::kTensorBytes : 0) + ii * 1024;
                     // Keep the 32-bit lane offset opaque so the address stays
                     // "SGPR base + VGPR offset" instead of a hoisted 64-bit sum.
-                    uint32_t lb = lane_base[i];
+                    uint32_t lb = lane_base[i % kLBPeriod];
                     asm volatile("" : "+v"(lb));
                     __builtin_amdgcn_global_load_lds(base + lb, (lds_void*)d, 16, 0, 0);
                 }
@@ -716,7 +732,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
                     const int ii = j % S::kInstrPerTensor;
                     const int kv = min(kv0 + ii * S::kRowsPerInstr + lr, kv_len - 1);
                     const uint32_t off = (uint32_t)kv * S::kRowBytes +
-                                         (lane_base[i] - (uint32_t)(lr * S::kRowBytes));
+                                         (lane_base[i % kLBPeriod] - (uint32_t)(lr * S::kRowBytes));
                     char* d = dst + (is_v ? S::kTensorBytes : 0) + ii * 1024;
                     __builtin_amdgcn_global_load_lds((is_v ? Vh : Kh) + off, (lds_void*)d, 16, 0, 0);
                 }

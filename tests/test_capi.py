@@ -142,8 +142,9 @@ def test_plans_for_baseline_configs():
     rows_per_block = p.block_threads // 64 * 32      # 32 query rows per wave
     assert p.path == "prefill" and p.rows_per_group == 4 * 4096
     assert p.grid_blocks == 8 * (4 * 4096 // rows_per_block)
-    p = kf.plan(1, 512, 512, 32, 8, 128)             # C1
-    assert p.path == "prefill" and p.grid_blocks == 8 * (4 * 512 // rows_per_block)
+    p = kf.plan(1, 512, 512, 32, 8, 128)             # C1: 64 8-wave blocks would idle CUs
+    assert p.path == "prefill" and p.block_threads == 128
+    assert p.grid_blocks == 8 * (4 * 512 // 64) == 256
     assert p.workspace_bytes == 0
     p = kf.plan(1, 1, 4096, 32, 8, 128)              # C2 decode
     assert p.path == "decode_split" and p.rows_per_group == 4
@@ -171,6 +172,24 @@ def test_decode_split_geometry_covers_kv(B, q, kv, H_q, H_kv, D):
         parts = B * H_q * q * p.num_splits
         assert p.workspace_bytes >= parts * (D + 2) * 4
         assert p.num_splits <= 1024
+
+
+@pytest.mark.parametrize("S,H_kv,D,waves", [
+    (4096, 8, 128, 8), (2048, 8, 128, 8), (1024, 8, 128, 4), (512, 8, 128, 2), (256, 8, 128, 2),
+    (2048, 1, 64, 8), (130, 2, 256, 4), (4096, 8, 256, 4),
+])
+def test_prefill_waves_per_workgroup(S, H_kv, D, waves):
+    """Waves per workgroup: the most the head dimension allows (8, or 4 at
+    D = 256), halved down to 2 (4 at D = 256) while the grid would give fewer
+    workgroups than the 256 CUs."""
+    p = kf.plan(1, S, S, 32, H_kv, D)
+    assert p.path == "prefill" and p.block_threads == 64 * waves
+    R = 32 // H_kv * S
+    assert p.grid_blocks == H_kv * -(-R // (32 * waves))
+    if waves > (4 if D == 256 else 2):
+        assert p.grid_blocks >= 256
+    if waves < (4 if D == 256 else 8):
+        assert H_kv * -(-R // (64 * waves)) < 256
 
 
 def test_prefill_threshold():
