@@ -13,6 +13,11 @@
 //       separate q_len / kv_len, caller-owned Mi / Li).  Split-KV workspace is
 //       cached per host thread and grown on demand; it is never allocated
 //       inside a steady-state loop once the largest shape has been seen.
+//
+//   kf::attn_fwd_ex(...), kf::attn_decode_paged(...)
+//       the same over kf_attn_fwd_ex / kf_attn_decode_paged (causal masking,
+//       per-sequence key counts, paged K/V, fp16 / bf16 O, LSE), which have
+//       no counterpart in the reference.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -85,3 +90,44 @@ inline hipError_t launch_flash_attn(const uint16_t* Q, const uint16_t* K, const 
                      static_cast<void*>(stream));
     return kf::status_to_hip(st);
 }
+
+namespace kf {
+
+// kf_attn_fwd_ex with the per-thread cached workspace: kv_lens (device int[B]
+// or nullptr) and flags (KF_ATTN_CAUSAL, KF_ATTN_OUT_F16 / _BF16,
+// KF_ATTN_LSE) as documented in kf/attn.h.
+inline hipError_t attn_fwd_ex(const uint16_t* Q, const uint16_t* K, const uint16_t* V, void* O,
+                              int B, int q_len, int kv_len, int H_q, int H_kv, int D,
+                              const int* kv_lens, int flags, hipStream_t stream,
+                              float* Mi = nullptr, float* Li = nullptr) {
+    kf_attn_plan_t plan;
+    int st = kf_attn_plan(B, q_len, kv_len, H_q, H_kv, D, &plan);
+    if (st != KF_OK) return status_to_hip(st);
+    WorkspaceCache& ws = thread_workspace();
+    hipError_t e = ws.reserve(plan.workspace_bytes);
+    if (e != hipSuccess) return e;
+    st = kf_attn_fwd_ex(Q, K, V, O, Mi, Li, B, q_len, kv_len, H_q, H_kv, D, kv_lens, flags,
+                        ws.ptr, ws.bytes, static_cast<void*>(stream));
+    return status_to_hip(st);
+}
+
+// kf_attn_decode_paged with the per-thread cached workspace.
+inline hipError_t attn_decode_paged(const uint16_t* Q, const uint16_t* K_pages,
+                                    const uint16_t* V_pages, const int* block_table,
+                                    const int* kv_lens, void* O, int B, int q_len, int H_q,
+                                    int H_kv, int D, int page_size, int max_pages_per_seq,
+                                    int num_pages, int flags, hipStream_t stream,
+                                    float* Mi = nullptr, float* Li = nullptr) {
+    const size_t need = kf_attn_decode_paged_workspace_bytes(B, q_len, H_q, H_kv, D, page_size,
+                                                             max_pages_per_seq);
+    WorkspaceCache& ws = thread_workspace();
+    hipError_t e = ws.reserve(need);
+    if (e != hipSuccess) return e;
+    const int st = kf_attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, O, Mi, Li, B,
+                                        q_len, H_q, H_kv, D, page_size, max_pages_per_seq,
+                                        num_pages, flags, ws.ptr, ws.bytes,
+                                        static_cast<void*>(stream));
+    return status_to_hip(st);
+}
+
+}  // namespace kf

@@ -145,6 +145,85 @@ static bool run_case(int B, int q_len, int kv_len, int H_q, int H_kv, int D, uin
     return ok;
 }
 
+// The extensions through kf/flash_attn.hpp, checked for exact agreement with
+// the paths above: kf::attn_fwd_ex without masking and with every key count
+// equal to kv_len, paged decode over pages holding the cache rows in order,
+// and an fp16 O equal to the round-to-nearest-even of the fp32 O.
+static bool run_extension_checks() {
+    const int B = 2, H_q = 32, H_kv = 8, D = 128, q_len = 1, kv_len = 1024, page = 16;
+    const int pages = kv_len / page;
+    const size_t qn = (size_t)B * H_q * q_len * D, kvn = (size_t)B * H_kv * kv_len * D;
+    std::mt19937 rng(777);
+    std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
+    std::vector<uint16_t> q16(qn), k16(kvn), v16(kvn);
+    for (auto& x : q16) x = kf_oracle_float_to_half(dist(rng));
+    for (auto& x : k16) x = kf_oracle_float_to_half(dist(rng));
+    for (auto& x : v16) x = kf_oracle_float_to_half(dist(rng));
+    // Pool page b * pages + p holds rows [p * page, (p + 1) * page) of sequence b.
+    std::vector<uint16_t> kp(kvn), vp(kvn);
+    for (int b = 0; b < B; ++b)
+        for (int h = 0; h < H_kv; ++h)
+            for (int j = 0; j < kv_len; ++j) {
+                const size_t src = (((size_t)b * H_kv + h) * kv_len + j) * D;
+                const size_t dst = ((((size_t)b * pages + j / page) * H_kv + h) * page + j % page) * D;
+                std::copy(k16.begin() + src, k16.begin() + src + D, kp.begin() + dst);
+                std::copy(v16.begin() + src, v16.begin() + src + D, vp.begin() + dst);
+            }
+    std::vector<int> table(B * pages), lens(B, kv_len);
+    for (int i = 0; i < B * pages; ++i) table[i] = i;
+
+    uint16_t *dq, *dk, *dv, *dkp, *dvp, *dO16;
+    int *dtab, *dlen;
+    float *dO0, *dO1, *dO2;
+    HIP_CHECK(hipMalloc(&dq, qn * 2));
+    HIP_CHECK(hipMalloc(&dk, kvn * 2));
+    HIP_CHECK(hipMalloc(&dv, kvn * 2));
+    HIP_CHECK(hipMalloc(&dkp, kvn * 2));
+    HIP_CHECK(hipMalloc(&dvp, kvn * 2));
+    HIP_CHECK(hipMalloc(&dtab, table.size() * 4));
+    HIP_CHECK(hipMalloc(&dlen, lens.size() * 4));
+    HIP_CHECK(hipMalloc(&dO0, qn * 4));
+    HIP_CHECK(hipMalloc(&dO1, qn * 4));
+    HIP_CHECK(hipMalloc(&dO2, qn * 4));
+    HIP_CHECK(hipMalloc(&dO16, qn * 2));
+    HIP_CHECK(hipMemcpy(dq, q16.data(), qn * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dk, k16.data(), kvn * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dv, v16.data(), kvn * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dkp, kp.data(), kvn * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dvp, vp.data(), kvn * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dtab, table.data(), table.size() * 4, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dlen, lens.data(), lens.size() * 4, hipMemcpyHostToDevice));
+
+    HIP_CHECK(launch_flash_attn(dq, dk, dv, dO0, B, q_len, kv_len, H_q, H_kv, D, nullptr));
+    HIP_CHECK(kf::attn_fwd_ex(dq, dk, dv, dO1, B, q_len, kv_len, H_q, H_kv, D, dlen, 0, nullptr));
+    HIP_CHECK(kf::attn_decode_paged(dq, dkp, dvp, dtab, dlen, dO2, B, q_len, H_q, H_kv, D, page,
+                                    pages, B * pages, 0, nullptr));
+    HIP_CHECK(kf::attn_fwd_ex(dq, dk, dv, dO16, B, q_len, kv_len, H_q, H_kv, D, nullptr,
+                              KF_ATTN_OUT_F16, nullptr));
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<float> o0(qn), o1(qn), o2(qn);
+    std::vector<uint16_t> o16(qn);
+    HIP_CHECK(hipMemcpy(o0.data(), dO0, qn * 4, hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(o1.data(), dO1, qn * 4, hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(o2.data(), dO2, qn * 4, hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(o16.data(), dO16, qn * 2, hipMemcpyDeviceToHost));
+    for (void* ptr : {(void*)dq, (void*)dk, (void*)dv, (void*)dkp, (void*)dvp, (void*)dtab,
+                      (void*)dlen, (void*)dO0, (void*)dO1, (void*)dO2, (void*)dO16})
+        (void)hipFree(ptr);
+
+    size_t bad_lens = 0, bad_paged = 0, bad_f16 = 0;
+    for (size_t i = 0; i < qn; ++i) {
+        bad_lens += o1[i] != o0[i];
+        bad_paged += o2[i] != o0[i];
+        bad_f16 += o16[i] != kf_oracle_float_to_half(o0[i]);
+    }
+    const bool ok = bad_lens == 0 && bad_paged == 0 && bad_f16 == 0;
+    std::printf("  B=%d q_len=1 kv_len=%d GQA %d:%d D=%d page=%d ... %s (differing elements: "
+                "key counts %zu, paged %zu, fp16 O %zu)\n",
+                B, kv_len, H_q, H_kv, D, page, ok ? "PASS" : "FAIL", bad_lens, bad_paged, bad_f16);
+    return ok;
+}
+
 int main() {
     std::printf("=== kernelfoundry_amd flash-attention end-to-end tests (gfx950) ===\n");
     int failed = 0;
@@ -173,6 +252,9 @@ int main() {
     };
     for (const DC& c : dec_cases)
         if (!run_case(c.B, c.q_len, c.kv_len, c.H_q, c.H_kv, c.D, c.seed, false)) ++failed;
+
+    std::printf("[extensions through kf/flash_attn.hpp: exact agreement]\n");
+    if (!run_extension_checks()) ++failed;
 
     if (failed) {
         std::printf("%d test(s) FAILED\n", failed);
