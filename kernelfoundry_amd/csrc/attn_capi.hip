@@ -7,8 +7,6 @@
 
 #include <climits>
 #include <cstdint>
-#include <cstdio>
-#include <cstdlib>
 
 #include "attn_kernels.h"
 #include "kf/attn.h"
@@ -22,7 +20,6 @@ constexpr int kDecodeMinSplitRows = 4 * kf::kDecodeStage;  // one stage per wave
 constexpr size_t kWsAlign = 256;
 
 thread_local int g_last_hip_error = 0;
-
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 

@@ -3,16 +3,21 @@
 // Three kernels, all hand-written for wave64 and the fp16 MFMA
 // v_mfma_f32_32x32x16_f16:
 //
-//   kf_attn_prefill_kernel<D>  one workgroup = 8 waves (4 for D = 256) x 32
-//                              query rows of one KV head; K/V streamed
-//                              HBM -> LDS by LDS-DMA through a ring of LDS
-//                              stages; online softmax in registers.
-//   kf_attn_decode_kernel<D>   split-KV ("flash-decoding") for <= 32 query
+//   kf_attn_prefill_kernel<D, kMask, NW>
+//                              one workgroup = NW waves x 32 query rows of
+//                              one KV head (NW = 8, 4 for D = 256, fewer for
+//                              small grids); K/V streamed HBM -> LDS by
+//                              LDS-DMA through a ring of LDS stages; online
+//                              softmax in registers; kMask adds causal
+//                              masking / per-sequence key counts.
+//   kf_attn_decode_kernel<D, kPaged>
+//                              split-KV ("flash-decoding") for <= 32 query
 //                              rows per KV head (Q_len = 1 decode, GQA/MQA
 //                              groups): every wave streams its own KV stages
 //                              through a wave-private LDS slot; the 4 waves of
 //                              a workgroup merge in LDS; with several splits
-//                              each workgroup writes an unnormalised partial.
+//                              each workgroup writes an unnormalised partial;
+//                              kPaged reads K/V through a block table.
 //   kf_attn_split_merge_kernel<D>  merges the split partials into O, Mi, Li.
 //
 // Behaviour follows the reference forward (kernels/flash_attn.cu:384-585):
@@ -80,7 +85,7 @@ struct AttnParams {
     float* Lpart;       // [B * H_kv][n_splits][R]  sum of exp relative to Mpart
     int rows_per_group; // R = (H_q / H_kv) * q_len
     int kv_len;
-    int row_tiles;      // prefill: ceil(R / 128)
+    int row_tiles;      // prefill: ceil(R / rows per workgroup)
     int n_splits;       // decode: KV partitions per group
     int kv_per_split;   // decode: multiple of 32
     int rows_total;     // B * H_q * q_len
@@ -449,7 +454,7 @@ __device__ __forceinline__ void pv_accum(const f16* __restrict__ Vt, int kv0,
 }
 
 // ---------------------------------------------------------------------------
-// Prefill: 8 waves (D = 256: 4) x 32 query rows per workgroup.  K and V
+// Prefill: NW waves x 32 query rows per workgroup.  K and V
 // stages are copied HBM -> LDS by the gfx950 LDS-DMA loads
 // (global_load_lds_dwordx4: each wave instruction fills one contiguous KiB
 // of LDS, no VGPR staging) into named LDS arrays, so the prefetch of later
@@ -500,11 +505,10 @@ template <int D, int NW = kPrefillMaxWaves<D>> struct PrefillCfg {
     // whatever the workgroup size, so every variant keeps its accumulators in
     // VGPRs; 512 for D = 256.
     static constexpr int kWavesPerEU = D >= 256 ? 1 : 2;
-    static constexpr bool kPipeline = D <= 128;
     // Pipelined: stages t, t+1 and the one being filled rotate through three
     // LDS buffers; otherwise two suffice (and keep every LDS offset of D = 256
     // inside the 16-bit instruction offset field).
-    static constexpr int kBuffers = kPipeline ? 3 : 2;
+    static constexpr bool kPipeline = D <= 128;
     // Tiles per LDS stage.  Pipelined 8-wave workgroups hold two tiles per
     // stage, so the workgroup barrier and the LDS-DMA issue come once per 64
     // kv rows.  Smaller workgroups keep one tile per stage: their LDS (48 KB
