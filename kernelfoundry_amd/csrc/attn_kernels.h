@@ -1177,12 +1177,12 @@ void kf_attn_decode_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Split merge: one workgroup per query row.  Phase 1 stages every split's
-// (M_k, l_k) for the row in LDS and turns them into weights
-// w_k = exp(M_k - max_k M_k); phase 2 spreads the splits over kLanes groups
-// of threads (each thread owns 4 consecutive d for splits k = lane, lane +
-// kLanes, ...) so every thread has only a few independent loads in flight,
-// then reduces the kLanes partial sums in LDS.
+// Split merge: one workgroup per query row.  Phase 1 turns every split's
+// (M_k, l_k) for the row into weights w_k = exp(M_k - max_k M_k) staged in
+// LDS; phase 2 spreads the splits over kLanes groups of threads (each thread
+// owns 4 consecutive d for splits k = lane, lane + kLanes, ...) and reduces
+// the kLanes partial sums in LDS.  The first loads of both phases are issued
+// together, so small split counts cost one memory round trip.
 //   O = sum_k w_k O_k / sum_k w_k l_k,  Mi = max_k M_k,  Li = sum_k w_k l_k.
 // ---------------------------------------------------------------------------
 constexpr int kMergeThreads = 256;
@@ -1203,10 +1203,30 @@ void kf_attn_split_merge_kernel(AttnParams p) {
     const int grp = row / R, r = row % R;
     const int ns = p.n_splits;
     const size_t base = (size_t)grp * ns * R + r;  // partial index of split 0
+    const int lane = tid / kD4, d4 = tid % kD4;
+    const float* Ob = p.Opart + base * D + 4 * d4;
 
-    // Phase 1: max over splits.
-    float m = -INFINITY;
-    for (int k = tid; k < ns; k += kMergeThreads) {
+    // Issue the first loads of both phases together (the first split of M and
+    // L per thread, the first 4 partial-O vectors per split lane), so that up
+    // to kMergeThreads splits (M, L) and 4 * kLanes splits (O) cost one
+    // memory round trip instead of three.
+    constexpr int kPre = 4;
+    f32x4 opre[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+        const int k = lane + i * kLanes;
+        opre[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (k < ns) opre[i] = *reinterpret_cast<const f32x4*>(Ob + (size_t)k * R * D);
+    }
+    float m0 = -INFINITY, l0 = 0.f;
+    if (tid < ns) {
+        m0 = p.Mpart[base + (size_t)tid * R];
+        l0 = p.Lpart[base + (size_t)tid * R];
+    }
+
+    // Phase 1: max over splits, weights w_k = exp(M_k - max), l = sum w_k l_k.
+    float m = m0;
+    for (int k = tid + kMergeThreads; k < ns; k += kMergeThreads) {
         const float mk = p.Mpart[base + (size_t)k * R];
         s_w[k] = mk;
         m = fmaxf(m, mk);
@@ -1216,9 +1236,14 @@ void kf_attn_split_merge_kernel(AttnParams p) {
     if ((tid & 63) == 0) s_red[tid >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    float lsum = 0.f;
     const bool none = m == -INFINITY;  // no split saw a key for this row
-    for (int k = tid; k < ns; k += kMergeThreads) {
+    float lsum = 0.f;
+    if (tid < ns) {
+        const float w = none ? 0.f : exp2_hw((m0 - m) * kLog2e);
+        s_w[tid] = w;
+        lsum = w * l0;
+    }
+    for (int k = tid + kMergeThreads; k < ns; k += kMergeThreads) {
         const float w = none ? 0.f : exp2_hw((s_w[k] - m) * kLog2e);
         s_w[k] = w;
         lsum += w * p.Lpart[base + (size_t)k * R];
@@ -1231,10 +1256,13 @@ void kf_attn_split_merge_kernel(AttnParams p) {
     const float l = s_red[0] + s_red[1] + s_red[2] + s_red[3];
 
     // Phase 2: weighted sum of the partial outputs.
-    const int lane = tid / kD4, d4 = tid % kD4;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    const float* Ob = p.Opart + base * D + 4 * d4;
-    int k = lane;
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+        const int k = lane + i * kLanes;
+        if (k < ns) acc += s_w[k] * opre[i];
+    }
+    int k = lane + kPre * kLanes;
     for (; k + 3 * kLanes < ns; k += 4 * kLanes) {
         const f32x4 o0 = *reinterpret_cast<const f32x4*>(Ob + (size_t)k * R * D);
         const f32x4 o1 = *reinterpret_cast<const f32x4*>(Ob + (size_t)(k + kLanes) * R * D);
