@@ -60,7 +60,7 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) 
         long long splits = (kDecodeTargetBlocks + n_groups - 1) / n_groups;
         const long long max_splits = (kv_len + kDecodeMinSplitRows - 1) / kDecodeMinSplitRows;
         if (splits > max_splits) splits = max_splits;
-        if (splits > kf::kMergeMaxSplits) splits = kf::kMergeMaxSplits;
+        if (splits > kf::merge_max_splits(D)) splits = kf::merge_max_splits(D);
         if (splits < 1) splits = 1;
         long long per = (kv_len + splits - 1) / splits;
         per = (per + kf::kDecodeStage - 1) / kf::kDecodeStage * kf::kDecodeStage;

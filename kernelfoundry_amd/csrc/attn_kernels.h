@@ -1177,23 +1177,28 @@ void kf_attn_decode_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Split merge: one workgroup per query row.  Phase 1 turns every split's
-// (M_k, l_k) for the row into weights w_k = exp(M_k - max_k M_k) staged in
-// LDS; phase 2 spreads the splits over kLanes groups of threads (each thread
-// owns 4 consecutive d for splits k = lane, lane + kLanes, ...) and reduces
-// the kLanes partial sums in LDS.  The first loads of both phases are issued
-// together, so small split counts cost one memory round trip.
+// Split merge: one workgroup per query row.  Thread t < ns reads split t's
+// (M_t, l_t) and turns it into the weight w_t = exp(M_t - max_k M_k), staged
+// in LDS; the partial outputs are spread over kLanes groups of threads (each
+// thread owns 4 consecutive d and the splits lane + i * kLanes, i < kPre) and
+// the kLanes partial sums reduced in LDS.  Every load is issued before the
+// first reduction, so the merge costs one memory round trip.  The planner
+// never makes more splits than merge_max_splits(D) = kPre * kLanes (<= 256).
 //   O = sum_k w_k O_k / sum_k w_k l_k,  Mi = max_k M_k,  Li = sum_k w_k l_k.
 // ---------------------------------------------------------------------------
 constexpr int kMergeThreads = 256;
-constexpr int kMergeMaxSplits = 1024;
+constexpr int kMergePre = 4;  // partial-O vectors per thread
+
+constexpr int merge_max_splits(int D) { return kMergePre * (kMergeThreads / (D / 4)); }
 
 template <int D>
 __global__ __launch_bounds__(kMergeThreads)
 void kf_attn_split_merge_kernel(AttnParams p) {
     constexpr int kD4 = D / 4;                     // float4 columns per row
     constexpr int kLanes = kMergeThreads / kD4;    // split lanes
-    __shared__ float s_w[kMergeMaxSplits];
+    constexpr int kPre = kMergePre;
+    static_assert(merge_max_splits(D) <= kMergeThreads, "one split per thread in phase 1");
+    __shared__ float s_w[kMergeThreads];
     __shared__ float s_red[kMergeThreads / 64];
     __shared__ f32x4 s_acc[kLanes][kD4];
 
@@ -1201,16 +1206,11 @@ void kf_attn_split_merge_kernel(AttnParams p) {
     const int row = blockIdx.x;                    // global query row
     const int R = p.rows_per_group;
     const int grp = row / R, r = row % R;
-    const int ns = p.n_splits;
+    const int ns = p.n_splits;                     // <= merge_max_splits(D)
     const size_t base = (size_t)grp * ns * R + r;  // partial index of split 0
     const int lane = tid / kD4, d4 = tid % kD4;
     const float* Ob = p.Opart + base * D + 4 * d4;
 
-    // Issue the first loads of both phases together (the first split of M and
-    // L per thread, the first 4 partial-O vectors per split lane), so that up
-    // to kMergeThreads splits (M, L) and 4 * kLanes splits (O) cost one
-    // memory round trip instead of three.
-    constexpr int kPre = 4;
     f32x4 opre[kPre];
 #pragma unroll
     for (int i = 0; i < kPre; ++i) {
@@ -1224,13 +1224,8 @@ void kf_attn_split_merge_kernel(AttnParams p) {
         l0 = p.Lpart[base + (size_t)tid * R];
     }
 
-    // Phase 1: max over splits, weights w_k = exp(M_k - max), l = sum w_k l_k.
+    // Max over splits, weights, l = sum w_k l_k.
     float m = m0;
-    for (int k = tid + kMergeThreads; k < ns; k += kMergeThreads) {
-        const float mk = p.Mpart[base + (size_t)k * R];
-        s_w[k] = mk;
-        m = fmaxf(m, mk);
-    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if ((tid & 63) == 0) s_red[tid >> 6] = m;
@@ -1243,11 +1238,6 @@ void kf_attn_split_merge_kernel(AttnParams p) {
         s_w[tid] = w;
         lsum = w * l0;
     }
-    for (int k = tid + kMergeThreads; k < ns; k += kMergeThreads) {
-        const float w = none ? 0.f : exp2_hw((s_w[k] - m) * kLog2e);
-        s_w[k] = w;
-        lsum += w * p.Lpart[base + (size_t)k * R];
-    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off);
     __syncthreads();  // s_red reuse; s_w complete
@@ -1255,23 +1245,13 @@ void kf_attn_split_merge_kernel(AttnParams p) {
     __syncthreads();
     const float l = s_red[0] + s_red[1] + s_red[2] + s_red[3];
 
-    // Phase 2: weighted sum of the partial outputs.
+    // Weighted sum of the partial outputs.
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < kPre; ++i) {
         const int k = lane + i * kLanes;
         if (k < ns) acc += s_w[k] * opre[i];
     }
-    int k = lane + kPre * kLanes;
-    for (; k + 3 * kLanes < ns; k += 4 * kLanes) {
-        const f32x4 o0 = *reinterpret_cast<const f32x4*>(Ob + (size_t)k * R * D);
-        const f32x4 o1 = *reinterpret_cast<const f32x4*>(Ob + (size_t)(k + kLanes) * R * D);
-        const f32x4 o2 = *reinterpret_cast<const f32x4*>(Ob + (size_t)(k + 2 * kLanes) * R * D);
-        const f32x4 o3 = *reinterpret_cast<const f32x4*>(Ob + (size_t)(k + 3 * kLanes) * R * D);
-        acc += s_w[k] * o0 + s_w[k + kLanes] * o1 + s_w[k + 2 * kLanes] * o2 +
-               s_w[k + 3 * kLanes] * o3;
-    }
-    for (; k < ns; k += kLanes) acc += s_w[k] * *reinterpret_cast<const f32x4*>(Ob + (size_t)k * R * D);
     s_acc[lane][d4] = acc;
     __syncthreads();
     if (tid < kD4) {

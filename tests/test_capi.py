@@ -171,7 +171,20 @@ def test_decode_split_geometry_covers_kv(B, q, kv, H_q, H_kv, D):
     else:
         parts = B * H_q * q * p.num_splits
         assert p.workspace_bytes >= parts * (D + 2) * 4
-        assert p.num_splits <= 1024
+        # The split merge reads every partial in one pass: 4 per thread.
+        assert p.num_splits <= 4 * (256 // (D // 4))
+
+
+@pytest.mark.parametrize("B,H_kv,kv,D,splits", [
+    (1, 8, 131072, 128, 32), (1, 1, 262144, 128, 32), (1, 1, 65536, 64, 64),
+    (1, 1, 1 << 20, 16, 256), (1, 4, 40000, 256, 16), (1, 8, 8192, 128, 32),
+])
+def test_decode_splits_capped_at_merge_capacity(B, H_kv, kv, D, splits):
+    """Few KV groups over a long KV want more splits than the merge kernel
+    reads in one pass; the plan stops at that capacity (4096 / D splits)."""
+    p = kf.plan(B, 1, kv, 32, H_kv, D)
+    assert p.path == "decode_split" and p.num_splits == splits
+    assert p.num_splits * p.kv_per_split >= kv
 
 
 @pytest.mark.parametrize("S,H_kv,D,waves", [

