@@ -96,6 +96,24 @@ class Plan:
 _lib = None
 
 
+def _bind_torch_hip_runtime():
+    """Load torch's HIP runtime before libkf_attn.so, if torch is installed.
+
+    PyTorch-ROCm wheels ship their own libamdhip64 / libhsa-runtime64, which
+    torch loads by the unversioned name; libkf_attn.so asks for
+    libamdhip64.so.7 (soname of both copies).  Loaded after torch, the
+    library binds to torch's runtime by soname.  Loaded before torch, it pulls
+    in the system runtime and torch then adds its own: two HIP and two HSA
+    runtimes in one process, torch's tensors and streams living in the one
+    and this library's launches in the other (seen as failed launches and
+    crashes).  Importing torch first keeps one runtime.
+    """
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def load_library(path: str = LIB_PATH):
     """Load libkf_attn.so; raises if it has not been built."""
     global _lib
@@ -105,6 +123,7 @@ def load_library(path: str = LIB_PATH):
         raise RuntimeError(
             f"{path} is missing: build it with `python -m kernelfoundry_amd.build` "
             "(or __graft_entry__.build()); there is no fallback implementation")
+    _bind_torch_hip_runtime()
     lib = ctypes.CDLL(path)
     i, p, sz = ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
     lib.kf_attn_plan.argtypes = [i] * 6 + [ctypes.POINTER(_PlanStruct)]

@@ -122,12 +122,13 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
         if constexpr (D >= 256) {
             launch_prefill<D, 4>(pl, prm, mask, stream);
         } else {
-            if (pl.waves == 8)
+            if (pl.waves == 8) {
                 launch_prefill<D, 8>(pl, prm, mask, stream);
-            else if (pl.waves == 4)
+            } else if (pl.waves == 4) {
                 launch_prefill<D, 4>(pl, prm, mask, stream);
-            else
+            } else {
                 launch_prefill<D, 2>(pl, prm, mask, stream);
+            }
         }
         return hipGetLastError();
     }

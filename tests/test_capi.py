@@ -255,3 +255,25 @@ def test_paged_decode_validation():
     assert _paged(ws_bytes=need - 1) == kf.KF_ERR_WORKSPACE
     assert kf.paged_workspace_bytes(2, 9, 32, 8, 128, 16, 64) == 0    # not a decode shape
     assert kf.paged_workspace_bytes(2, 1, 32, 8, 128, 24, 64) == 0    # bad page size
+
+
+def test_library_loaded_before_torch_keeps_one_hip_runtime():
+    """kf.plan() before `import torch` must not leave two HIP / HSA runtimes
+    in the process (the library's system libamdhip64.so.7 and the copy
+    torch's wheel loads by its unversioned name): load_library() imports torch
+    first.  Checked in a fresh interpreter through /proc/self/maps."""
+    import subprocess
+    import sys
+    pytest.importorskip("torch")
+    code = (
+        "import re, kernelfoundry_amd as kf\n"
+        "kf.plan(1, 1, 4096, 32, 8, 128)\n"
+        "import torch\n"
+        "m = open('/proc/self/maps').read()\n"
+        "print(len(set(re.findall(r'\\S*libamdhip64\\S*', m))),"
+        " len(set(re.findall(r'\\S*libhsa-runtime64\\S*', m))))\n")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=root,
+                       timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert r.stdout.split() == ["1", "1"], r.stdout

@@ -232,10 +232,6 @@ def test_config_c5_batched_long_decode():
     _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (7, 9), (31, 31), (16, 4)])
 
 
-@pytest.mark.skip(reason="the process crashed (SIGSEGV in torch while pytest printed a GPU "
-                         "tensor of a failed kf.attn_fwd call; the exception itself was lost) "
-                         "on the first of these cases, when the plan still gave 64 / 512 splits; "
-                         "no cause shown yet, so the case stays off the GPU")
 @pytest.mark.parametrize("H_q,H_kv,kv", [(32, 8, 131072), (32, 1, 262144)])
 def test_long_context_decode(H_q, H_kv, kv):
     """One sequence of 128 K / 256 K keys (GQA and MQA with 32 query rows per
