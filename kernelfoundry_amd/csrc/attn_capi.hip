@@ -17,6 +17,7 @@ constexpr int kNumCUs = 256;            // MI355X compute units
 constexpr int kDecodeMaxRows = 32;      // query rows per KV head on the decode path
 constexpr int kDecodeTargetBlocks = 2 * kNumCUs;
 constexpr int kDecodeMinSplitRows = 4 * kf::kDecodeStage;  // one stage per wave
+constexpr int kMinGroupKeys = 128;      // keys before a prefill row's keys are split in two
 constexpr size_t kWsAlign = 256;
 
 thread_local int g_last_hip_error = 0;
@@ -36,6 +37,7 @@ struct Plan {
     int grid;
     int threads;
     int waves;          // prefill: waves per workgroup
+    int kv_groups;      // prefill: KV groups per workgroup (1 or 2)
     size_t ws_bytes;
     size_t ws_o_off, ws_m_off, ws_l_off;
 };
@@ -72,13 +74,22 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) 
         p.threads = kf::kDecodeThreads;
         p.path = splits > 1 ? KF_PATH_DECODE_SPLIT : KF_PATH_DECODE;
     } else {
-        // Waves per workgroup: the most the head dimension allows, halved
-        // (down to 2) while the grid would leave CUs without a workgroup.
-        // D = 256 stays at 4 waves (its accumulators need a SIMD per wave).
-        int nw = kf::prefill_max_waves(D);
-        const int nw_min = D >= 256 ? 4 : 2;
-        while (nw > nw_min && n_groups * ((R + 32 * nw - 1) / (32 * nw)) < kNumCUs) nw /= 2;
-        const int rows = 32 * nw;
+        // Waves per workgroup: the most the head dimension allows.  When that
+        // grid would leave CUs without a workgroup, D = 64 / 128 first split
+        // each row's keys between two KV groups of waves (8 waves x 128 rows,
+        // then 4 waves x 64 rows), which keeps two waves per SIMD; otherwise
+        // the waves are halved (down to 2).  D = 256 stays at 4 waves (its
+        // accumulators need a SIMD per wave).
+        int nw = kf::prefill_max_waves(D), ks = 1;
+        const auto wgs = [&](long long rows) { return n_groups * ((R + rows - 1) / rows); };
+        if ((D == 64 || D == 128) && wgs(32 * nw) < kNumCUs && kv_len >= kMinGroupKeys) {
+            ks = 2;
+            if (wgs(128) < kNumCUs) nw = 4;
+        } else {
+            const int nw_min = D >= 256 ? 4 : 2;
+            while (nw > nw_min && wgs(32 * nw) < kNumCUs) nw /= 2;
+        }
+        const int rows = 32 * nw / ks;
         const long long row_tiles = (R + rows - 1) / rows;
         if (n_groups * row_tiles > INT_MAX) return KF_ERR_SIZE;
         p.n_splits = 1;
@@ -87,6 +98,7 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) 
         p.grid = (int)(n_groups * row_tiles);
         p.threads = 64 * nw;
         p.waves = nw;
+        p.kv_groups = ks;
         p.path = KF_PATH_PREFILL;
     }
     if (p.path == KF_PATH_DECODE_SPLIT) {
@@ -107,12 +119,12 @@ int hip_fail(hipError_t e) {
     return KF_ERR_HIP;
 }
 
-template <int D, int NW>
+template <int D, int NW, int KS = 1>
 void launch_prefill(const Plan& pl, const kf::AttnParams& prm, bool mask, hipStream_t stream) {
     if (mask)
-        kf::kf_attn_prefill_kernel<D, true, NW><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+        kf::kf_attn_prefill_kernel<D, true, NW, KS><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
     else
-        kf::kf_attn_prefill_kernel<D, false, NW><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+        kf::kf_attn_prefill_kernel<D, false, NW, KS><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
 }
 
 template <int D>
@@ -122,6 +134,15 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
         if constexpr (D >= 256) {
             launch_prefill<D, 4>(pl, prm, mask, stream);
         } else {
+            if constexpr (D == 64 || D == 128) {
+                if (pl.kv_groups == 2) {
+                    if (pl.waves == 8)
+                        launch_prefill<D, 8, 2>(pl, prm, mask, stream);
+                    else
+                        launch_prefill<D, 4, 2>(pl, prm, mask, stream);
+                    return hipGetLastError();
+                }
+            }
             if (pl.waves == 8) {
                 launch_prefill<D, 8>(pl, prm, mask, stream);
             } else if (pl.waves == 4) {

@@ -490,17 +490,21 @@ template <> struct SwizzleRow<256> : SwizzleRow<128> {};
 // S(t+1) = K Q^T is overlapped with the softmax of tile t (that needs a second
 // score block in registers).  D = 256 holds 128 fp32 O accumulators per lane,
 // so it runs at most 4 waves (one per SIMD, up to 512 registers) without the
-// overlap.  Grids too small to give every CU a workgroup use fewer waves per
-// workgroup (NW = 4 or 2) so that more CUs take part.
+// overlap.  Grids too small to give every CU a workgroup use fewer rows per
+// workgroup: KS = 2 KV groups (each wave takes half of the keys of its rows,
+// the two halves merged in LDS at the end) and then fewer waves (NW = 4, 2).
 template <int D> constexpr int kPrefillMaxWaves = D >= 256 ? 4 : 8;
 
 constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
 
-template <int D, int NW = kPrefillMaxWaves<D>> struct PrefillCfg {
+template <int D, int NW = kPrefillMaxWaves<D>, int KS = 1> struct PrefillCfg {
     static constexpr int BC = 32;                   // KV rows per MFMA tile
     static constexpr int kWaves = NW;
+    static constexpr int kGroups = KS;              // KV groups per workgroup
+    static constexpr int kRowWaves = NW / KS;       // waves per KV group
     static constexpr int kThreads = 64 * kWaves;
-    static constexpr int kRows = 32 * kWaves;
+    static constexpr int kRows = 32 * kRowWaves;    // query rows per workgroup
+    static_assert(NW % KS == 0 && (KS == 1 || D <= 128), "KV groups: D <= 128");
     // Register budget: 256 per wave (two waves per SIMD) for D <= 128,
     // whatever the workgroup size, so every variant keeps its accumulators in
     // VGPRs; 512 for D = 256.
@@ -509,12 +513,12 @@ template <int D, int NW = kPrefillMaxWaves<D>> struct PrefillCfg {
     // LDS buffers; otherwise two suffice (and keep every LDS offset of D = 256
     // inside the 16-bit instruction offset field).
     static constexpr bool kPipeline = D <= 128;
-    // Tiles per LDS stage.  Pipelined 8-wave workgroups hold two tiles per
-    // stage, so the workgroup barrier and the LDS-DMA issue come once per 64
-    // kv rows.  Smaller workgroups keep one tile per stage: their LDS (48 KB
-    // at D = 128) then admits two waves per SIMD, which holds the compiler to
-    // the 256-register budget.
-    static constexpr int kSub = (kPipeline && kWaves >= 8) ? 2 : 1;
+    // Tiles per LDS stage.  Pipelined 8-wave workgroups without KV groups
+    // hold two tiles per stage, so the workgroup barrier and the LDS-DMA issue
+    // come once per 64 kv rows.  The others keep one tile per stage (48 KB of
+    // LDS per KV group at D = 128), which holds the compiler to the
+    // 256-register budget.
+    static constexpr int kSub = (kPipeline && kWaves >= 8 && KS == 1) ? 2 : 1;
     static constexpr int kStageRows = BC * kSub;
 };
 
@@ -610,29 +614,39 @@ __device__ __forceinline__ void block_update_max(RowState& st, float mx, float s
 
 // kMask: causal masking and/or per-sequence key counts (p.causal,
 // p.kv_lens); without it every row sees keys [0, kv_len).
-template <int D, bool kMask, int NW = kPrefillMaxWaves<D>>
-__global__ __launch_bounds__((PrefillCfg<D, NW>::kThreads), (PrefillCfg<D, NW>::kWavesPerEU))
+//
+// KS > 1 (KV groups): wave w works on row wave w % (NW / KS) of the
+// workgroup's rows and on KV group w / (NW / KS), i.e. on the tiles
+// [g tpg, (g+1) tpg) of the keys the workgroup needs.  Every group streams its
+// keys through its own region of each LDS stage buffer; all groups run the
+// same number of tiles (tiles past a group's keys are masked), so the
+// workgroup barriers line up.  At the end each group's (O, max, sum) is
+// rebased to its true max and group 0 merges them through LDS.
+template <int D, bool kMask, int NW = kPrefillMaxWaves<D>, int KS = 1>
+__global__ __launch_bounds__((PrefillCfg<D, NW, KS>::kThreads), (PrefillCfg<D, NW, KS>::kWavesPerEU))
 void kf_attn_prefill_kernel(AttnParams p) {
-    using Cfg = PrefillCfg<D, NW>;
+    using Cfg = PrefillCfg<D, NW, KS>;
     constexpr int BC = Cfg::BC;
     constexpr int kNSB = BC / 32;                 // 32-row score blocks per stage
-    constexpr int kPrefillWaves = Cfg::kWaves;
+    constexpr int kRowWaves = Cfg::kRowWaves;     // waves per KV group
     constexpr int kPrefillRows = Cfg::kRows;
     constexpr int kSub = Cfg::kSub;               // tiles per LDS stage
     constexpr int SR = Cfg::kStageRows;           // kv rows per LDS stage
-    using S = DmaStage<D, SR, kPrefillWaves>;
+    using S = DmaStage<D, SR, kRowWaves>;
     using SW = SwizzleRow<D>;
     constexpr int kNKK = D / 16;                  // MFMA k-steps over D
     constexpr int kNTD = (D < 32 ? 32 : D) / 32;  // 32-row O^T tiles
     constexpr bool kPipe = Cfg::kPipeline;
-    __shared__ __attribute__((aligned(1024))) char buf0[S::kStageBytes];
-    __shared__ __attribute__((aligned(1024))) char buf1[S::kStageBytes];
-    __shared__ __attribute__((aligned(1024))) char buf2[kPipe ? S::kStageBytes : 16];
+    __shared__ __attribute__((aligned(1024))) char buf0[KS * S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char buf1[KS * S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char buf2[kPipe ? KS * S::kStageBytes : 16];
     __shared__ __attribute__((aligned(16))) char zero_pad[16];  // D=16: V^T rows 16..31
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = KS == 1 ? wave_id : wave_id % kRowWaves;  // row wave
+    const int kgrp = KS == 1 ? 0 : wave_id / kRowWaves;        // KV group
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x);
     int rt = blk % p.row_tiles;
@@ -676,8 +690,18 @@ void kf_attn_prefill_kernel(AttnParams p) {
             }
         }
     }
-    const int ntiles = (blk_lim + BC - 1) / BC;   // 32-row tiles
-    const int nstages = (blk_lim + SR - 1) / SR;  // LDS stages
+    // KV group kgrp covers the keys [kv_base, kv_end) of the workgroup's
+    // range in tiles 0 .. ntiles - 1 (the same count for every group); row
+    // limits below are relative to kv_base.
+    const int ntiles_wg = (blk_lim + BC - 1) / BC;
+    const int ntiles = KS == 1 ? ntiles_wg : (ntiles_wg + KS - 1) / KS;  // 32-row tiles
+    const int nstages = (ntiles * BC + SR - 1) / SR;                     // LDS stages
+    const int kv_base = kgrp * ntiles * BC;
+    const int kv_end = min(kv_base + ntiles * BC, blk_lim);
+    if constexpr (KS > 1) wave_min = min(wave_min, kv_end) - kv_base;
+    char* const b0 = buf0 + kgrp * S::kStageBytes;  // this group's stage regions
+    char* const b1 = buf1 + kgrp * S::kStageBytes;
+    char* const b2 = buf2 + (kPipe ? kgrp * S::kStageBytes : 0);
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
     const char* Kh = reinterpret_cast<const char*>(p.K + (size_t)grp * kv_len * D);
@@ -693,24 +717,26 @@ void kf_attn_prefill_kernel(AttnParams p) {
     // row & 15 only, so instruction i repeats the offsets of instruction
     // i - kLBPeriod: kLaneBases distinct row phases, visited with stride W.
     constexpr int kLaneBases = S::kRowsPerInstr >= 16 ? 1 : 16 / S::kRowsPerInstr;
-    constexpr int kLBPeriod = kLaneBases / gcd_int(kPrefillWaves, kLaneBases);
+    constexpr int kLBPeriod = kLaneBases / gcd_int(kRowWaves, kLaneBases);
     uint32_t lane_base[kLBPeriod];
 #pragma unroll
     for (int i = 0; i < kLBPeriod; ++i) {
-        const int ii = (wave + kPrefillWaves * i) % S::kInstrPerTensor;
+        const int ii = (wave + kRowWaves * i) % S::kInstrPerTensor;
         const int lr = lane / S::kChunks;
         const int r = ii * S::kRowsPerInstr + lr;
         lane_base[i] = (uint32_t)(lr * S::kRowBytes +
                                   (((lane % S::kChunks) ^ SW::h(r)) % S::kChunks) * 16);
     }
-    auto issue_stage = [&](char* dst, int kv0) {
+    // kv0: first key of the stage relative to this group's kv_base.
+    auto issue_stage = [&](char* dst, int kv0_rel) {
+        const int kv0 = kv_base + kv0_rel;
         if (kv0 + SR <= kv_len) {
             // Full stage: wave-uniform row base (SGPRs) + the lane's constant
             // 32-bit offset; no per-lane address arithmetic.
 #pragma unroll
             for (int i = 0; i < S::kPerWave; ++i) {
-                const int j = wave + kPrefillWaves * i;
-                if (S::kInstrTotal % kPrefillWaves == 0 || j < S::kInstrTotal) {
+                const int j = wave + kRowWaves * i;
+                if (S::kInstrTotal % kRowWaves == 0 || j < S::kInstrTotal) {
                     const bool is_v = j >= S::kInstrPerTensor;
                     const int ii = j % S::kInstrPerTensor;
                     const char* base = (is_v ? Vh : Kh) +
@@ -730,8 +756,8 @@ void kf_attn_prefill_kernel(AttnParams p) {
             const int lr = lane / S::kChunks;
 #pragma unroll
             for (int i = 0; i < S::kPerWave; ++i) {
-                const int j = wave + kPrefillWaves * i;
-                if (S::kInstrTotal % kPrefillWaves == 0 || j < S::kInstrTotal) {
+                const int j = wave + kRowWaves * i;
+                if (S::kInstrTotal % kRowWaves == 0 || j < S::kInstrTotal) {
                     const bool is_v = j >= S::kInstrPerTensor;
                     const int ii = j % S::kInstrPerTensor;
                     const int kv = min(kv0 + ii * S::kRowsPerInstr + lr, kv_len - 1);
@@ -836,10 +862,11 @@ void kf_attn_prefill_kernel(AttnParams p) {
     // This lane's query row sees keys [0, lim_lane) (padding rows: blk_lim).
     int lim_lane = kv_len;
     if constexpr (kMask) lim_lane = row < R ? row_kv_limit(p, kvb, row % p.q_len) : blk_lim;
+    if constexpr (KS > 1) lim_lane = min(lim_lane, kv_end) - kv_base;
 
     // ---- Prologue: stage 0 (and 1 when pipelined) in flight, Q fragments, S(0). ----
-    issue_stage(buf0, 0);
-    if (kPipe && nstages > 1) issue_stage(buf1, SR);
+    issue_stage(b0, 0);
+    if (kPipe && nstages > 1) issue_stage(b1, SR);
     f16x8 qf[kNKK];
     load_q_frags<D>(Qg, row, R, lane, qf);
     if constexpr (D < 32) {
@@ -853,12 +880,12 @@ void kf_attn_prefill_kernel(AttnParams p) {
 #pragma unroll
     for (int td = 0; td < kNTD; ++td) o[td] = f32x16{};
     f32x16 sc[kNSB];
-    qk(buf0, qf, sc);
+    qk(b0, qf, sc);
     if (BC > wave_min) block_mask<kNSB>(sc, lim_lane, lane);
     block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, o);
     // Exponent offset; a row with no key yet (masked) keeps m = -inf and
     // must get P = 0, not NaN.
-    auto neg_m = [&]() { return (kMask && st.m == -INFINITY) ? 0.f : -st.m; };
+    auto neg_m = [&]() { return ((kMask || KS > 1) && st.m == -INFINITY) ? 0.f : -st.m; };
 
     // ---- One pipelined tile; S(t) and its running max are ready on entry.
     //   barrier; LDS-DMA of stage t+2
@@ -914,11 +941,11 @@ void kf_attn_prefill_kernel(AttnParams p) {
     };
     if constexpr (kPipe && kSub == 1) {
         for (int t = 0; t < ntiles; t += 3) {
-            tile(buf0, buf1, buf2, t, true);
+            tile(b0, b1, b2, t, true);
             if (t + 1 >= ntiles) break;
-            tile(buf1, buf2, buf0, t + 1, true);
+            tile(b1, b2, b0, t + 1, true);
             if (t + 2 >= ntiles) break;
-            tile(buf2, buf0, buf1, t + 2, true);
+            tile(b2, b0, b1, t + 2, true);
         }
     } else if constexpr (kPipe) {
         static_assert(kSub == 2, "pipelined stages hold one or two tiles");
@@ -926,24 +953,94 @@ void kf_attn_prefill_kernel(AttnParams p) {
         // buffer (t / 2) % 3; the loop body covers 3 stages.
         constexpr int H = BC * S::kRowBytes;
         for (int t = 0; t < ntiles; t += 6) {
-            tile(buf0, buf0 + H, nullptr, t, false);
+            tile(b0, b0 + H, nullptr, t, false);
             if (t + 1 >= ntiles) break;
-            tile(buf0 + H, buf1, buf2, t + 1, true);
+            tile(b0 + H, b1, b2, t + 1, true);
             if (t + 2 >= ntiles) break;
-            tile(buf1, buf1 + H, nullptr, t + 2, false);
+            tile(b1, b1 + H, nullptr, t + 2, false);
             if (t + 3 >= ntiles) break;
-            tile(buf1 + H, buf2, buf0, t + 3, true);
+            tile(b1 + H, b2, b0, t + 3, true);
             if (t + 4 >= ntiles) break;
-            tile(buf2, buf2 + H, nullptr, t + 4, false);
+            tile(b2, b2 + H, nullptr, t + 4, false);
             if (t + 5 >= ntiles) break;
-            tile(buf2 + H, buf0, buf1, t + 5, true);
+            tile(b2 + H, b0, b1, t + 5, true);
         }
     } else {
         for (int t = 0; t < ntiles; t += 2) {
-            tile(buf0, buf1, nullptr, t, false);
+            tile(b0, b1, nullptr, t, false);
             if (t + 1 >= ntiles) break;
-            tile(buf1, buf0, nullptr, t + 1, false);
+            tile(b1, b0, nullptr, t + 1, false);
         }
+    }
+
+    if constexpr (KS > 1) {
+        // ---- KV-group merge.  Each group rebases its state to its true row
+        // max: O_g, m_g = rmax scale (natural log), l_g (both half rows);
+        // a group that saw no key of a row has weight 0.  Groups 1 .. KS-1
+        // publish O_g in lane-private slots of the (now free) stage buffers
+        // and (m_g, l_g) in merge_ml; group 0 combines
+        //   O = sum_g w_g O_g / L, L = sum_g w_g l_g, w_g = exp(m_g - max_g m_g).
+        constexpr int kSlotFloats = kNTD * 16 * 64;      // one wave's O
+        constexpr int kSlots = (KS - 1) * kRowWaves;
+        static_assert(kSlotFloats * 4 <= S::kStageBytes && kSlots <= 3 * KS, "merge slots");
+        __shared__ float merge_ml[2 * kSlots * 64];
+        const float l_pair = st.l + __shfl_xor(st.l, 32);
+        const bool none = st.rmax == -INFINITY;
+        const float m_g = none ? -INFINITY : st.rmax * p.scale;
+        const float beta = none ? 0.f : exp2_hw(st.m - st.rmax * p.scale_log2);
+        auto slot = [&](int sidx) {
+            char* bb = sidx / KS == 0 ? buf0 : (sidx / KS == 1 ? buf1 : buf2);
+            return reinterpret_cast<float*>(bb + (sidx % KS) * S::kStageBytes);
+        };
+        __syncthreads();  // every group is done with its stage regions
+        if (kgrp > 0) {
+            const int sidx = (kgrp - 1) * kRowWaves + wave;
+            float* so = slot(sidx);
+#pragma unroll
+            for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) so[(td * 16 + r) * 64 + lane] = o[td][r] * beta;
+            merge_ml[sidx * 64 + lane] = m_g;
+            merge_ml[(kSlots + sidx) * 64 + lane] = l_pair * beta;
+        }
+        __syncthreads();
+        if (kgrp > 0) return;
+        float m_all = m_g;
+#pragma unroll
+        for (int gg = 1; gg < KS; ++gg) m_all = fmaxf(m_all, merge_ml[((gg - 1) * kRowWaves + wave) * 64 + lane]);
+        const float w0 = none ? 0.f : exp2_hw((m_g - m_all) * kLog2e) * beta;
+        float L = w0 * l_pair;
+#pragma unroll
+        for (int td = 0; td < kNTD; ++td) o[td] *= w0;
+#pragma unroll
+        for (int gg = 1; gg < KS; ++gg) {
+            const int sidx = (gg - 1) * kRowWaves + wave;
+            const float mo = merge_ml[sidx * 64 + lane];
+            const float wg = mo == -INFINITY ? 0.f : exp2_hw((mo - m_all) * kLog2e);
+            L += wg * merge_ml[(kSlots + sidx) * 64 + lane];
+            const float* so = slot(sidx);
+#pragma unroll
+            for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[td][r] += wg * so[(td * 16 + r) * 64 + lane];
+        }
+        if (row < R) {
+            const float inv = L > 0.f ? 1.0f / L : 0.f;
+            const size_t ri = (size_t)grp * R + row;
+#pragma unroll
+            for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int d = 32 * td + 8 * i + 4 * g;
+                    if (d < D) {
+                        f32x4 v = {o[td][4 * i] * inv, o[td][4 * i + 1] * inv,
+                                   o[td][4 * i + 2] * inv, o[td][4 * i + 3] * inv};
+                        store_out4(p, ri * D + d, v);
+                    }
+                }
+            if (g == 0) store_stats(p, ri, m_all, L);
+        }
+        return;
     }
 
     // ---- Epilogue: combine the two half-row partial sums, normalise, store. ----

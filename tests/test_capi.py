@@ -143,7 +143,7 @@ def test_plans_for_baseline_configs():
     assert p.path == "prefill" and p.rows_per_group == 4 * 4096
     assert p.grid_blocks == 8 * (4 * 4096 // rows_per_block)
     p = kf.plan(1, 512, 512, 32, 8, 128)             # C1: 64 8-wave blocks would idle CUs
-    assert p.path == "prefill" and p.block_threads == 128
+    assert p.path == "prefill" and p.block_threads == 256  # 2 row waves x 2 KV groups
     assert p.grid_blocks == 8 * (4 * 512 // 64) == 256
     assert p.workspace_bytes == 0
     p = kf.plan(1, 1, 4096, 32, 8, 128)              # C2 decode
@@ -187,22 +187,29 @@ def test_decode_splits_capped_at_merge_capacity(B, H_kv, kv, D, splits):
     assert p.num_splits * p.kv_per_split >= kv
 
 
-@pytest.mark.parametrize("S,H_kv,D,waves", [
-    (4096, 8, 128, 8), (2048, 8, 128, 8), (1024, 8, 128, 4), (512, 8, 128, 2), (256, 8, 128, 2),
-    (2048, 1, 64, 8), (130, 2, 256, 4), (4096, 8, 256, 4),
+@pytest.mark.parametrize("S,H_kv,D,waves,rows", [
+    (4096, 8, 128, 8, 256), (2048, 8, 128, 8, 256), (1024, 8, 128, 8, 128), (512, 8, 128, 4, 64),
+    (256, 8, 128, 4, 64), (100, 8, 128, 2, 64), (2048, 1, 64, 8, 256), (512, 1, 64, 4, 64), (1024, 1, 64, 8, 128),
+    (130, 2, 256, 4, 128), (4096, 8, 256, 4, 128),
 ])
-def test_prefill_waves_per_workgroup(S, H_kv, D, waves):
-    """Waves per workgroup: the most the head dimension allows (8, or 4 at
-    D = 256), halved down to 2 (4 at D = 256) while the grid would give fewer
-    workgroups than the 256 CUs."""
+def test_prefill_waves_per_workgroup(S, H_kv, D, waves, rows):
+    """Waves and query rows per workgroup: 8 waves x 256 rows (4 x 128 at
+    D = 256) when that grid gives every CU a workgroup.  Otherwise D = 64 / 128
+    split each row's keys between two KV groups of waves (8 waves x 128 rows,
+    then 4 x 64) if there are at least 128 keys, and the remaining cases
+    halve the waves (down to 2, or 4 at D = 256)."""
     p = kf.plan(1, S, S, 32, H_kv, D)
     assert p.path == "prefill" and p.block_threads == 64 * waves
     R = 32 // H_kv * S
-    assert p.grid_blocks == H_kv * -(-R // (32 * waves))
-    if waves > (4 if D == 256 else 2):
-        assert p.grid_blocks >= 256
-    if waves < (4 if D == 256 else 8):
-        assert H_kv * -(-R // (64 * waves)) < 256
+    assert p.grid_blocks == H_kv * -(-R // rows)
+    full = H_kv * -(-R // (256 if D <= 128 else 128)) >= 256
+    if full:
+        assert rows == (256 if D <= 128 else 128)
+    elif D <= 128 and S >= 128:
+        assert rows == 32 * waves // 2                      # two KV groups
+        assert rows == 64 or H_kv * -(-R // 128) >= 256
+    else:
+        assert rows == 32 * waves
 
 
 def test_prefill_threshold():

@@ -100,3 +100,37 @@ def test_prefill_8wave_masked_matches_unmasked_bitwise():
     O1 = kf.attn_fwd(Q, K, V, kv_lens=torch.full((B,), S, dtype=torch.int32, device="cuda"))
     torch.cuda.synchronize()
     assert torch.equal(O0, O1)
+
+
+# ---------------------------------------------------------------------------
+# KV groups: grids too small for 8-wave workgroups split each row's keys
+# between two groups of waves (8 waves x 128 rows, or 4 x 64), merged in LDS.
+# ---------------------------------------------------------------------------
+KV_GROUP_CASES = [
+    # B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens, threads, rows   what it hits
+    (1, 32, 8, 1024, 1024, 128, False, None, 512, 128),        # sweep S=1024: 8 waves x 2 groups
+    (1, 32, 8, 512, 512, 128, False, None, 256, 64),           # C1 shape: 4 waves x 2 groups
+    (1, 32, 8, 512, 130, 128, False, None, 256, 64),           # 5 tiles: groups of 3 and 2 (+ tail)
+    (1, 32, 8, 512, 128, 128, False, None, 256, 64),           # exactly 4 tiles
+    (2, 32, 8, 256, 300, 128, True, [300, 129], 256, 64),      # causal + key counts
+    (2, 32, 8, 256, 256, 128, True, [256, 40], 256, 64),       # second group sees no key
+    (1, 32, 1, 1024, 1024, 64, False, None, 512, 128),         # MQA D=64, 8 waves x 2 groups
+    (1, 32, 1, 512, 700, 64, True, None, 256, 64),             # MQA D=64 causal, q_len < kv_len
+]
+
+
+@pytest.mark.parametrize("case", KV_GROUP_CASES, ids=lambda c: "B{}_Hkv{}_q{}_kv{}_D{}_c{}_{}".format(
+    c[0], c[2], c[3], c[4], c[5], int(c[6]), "lens" if c[7] else "full"))
+def test_kv_groups_parity(case):
+    import kernelfoundry_amd as kf
+    B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens, threads, rows = case
+    pl = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
+    R = H_q // H_kv * q_len
+    assert pl.path == "prefill" and pl.block_threads == threads, pl
+    assert pl.grid_blocks == B * H_kv * -(-R // rows), pl       # two KV groups per workgroup
+    _announce(test="kv_groups", B=B, H_kv=H_kv, q_len=q_len, kv_len=kv_len, D=D, causal=causal,
+              kv_lens=kv_lens, grid=pl.grid_blocks)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, q_len, kv_len, D, 47000 + kv_len + D)
+    ref = orc.sdpa(q16, k16, v16, causal=causal, kv_lens=kv_lens)
+    got = _run(q16, k16, v16, causal, kv_lens)
+    _check(got, ref, f"case {case}")
