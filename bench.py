@@ -430,7 +430,7 @@ def main():
                    "baseline_config": "configs[2]"},
         "roofline": {
             "bound": "mfma",
-            "kernel": "kf_attn_prefill_kernel<128, false, 8>",
+            "kernel": "kf_attn_prefill_kernel<128, false, 8, 1>",
             "achieved": round(pre["kernel_tflops"], 2),
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
