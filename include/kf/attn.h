@@ -76,6 +76,9 @@ typedef struct kf_attn_plan_t {
     int grid_blocks;       /* workgroups of the main kernel                     */
     int block_threads;     /* threads per workgroup of the main kernel          */
     size_t workspace_bytes;/* bytes kf_attn_fwd needs in `workspace`            */
+    int splits_per_block;  /* decode: KV partitions per workgroup (4 = the
+                              short-split kernel, one partition per wave;
+                              1 = the streaming decode kernel); 0 on prefill    */
 } kf_attn_plan_t;
 
 /* Describe the dispatch kf_attn_fwd would use.  Validates like kf_attn_fwd

@@ -79,6 +79,7 @@ class _PlanStruct(ctypes.Structure):
         ("grid_blocks", ctypes.c_int),
         ("block_threads", ctypes.c_int),
         ("workspace_bytes", ctypes.c_size_t),
+        ("splits_per_block", ctypes.c_int),
     ]
 
 
@@ -91,6 +92,7 @@ class Plan:
     grid_blocks: int
     block_threads: int
     workspace_bytes: int
+    splits_per_block: int = 0
 
 
 _lib = None
@@ -166,7 +168,7 @@ def plan(B, q_len, kv_len, H_q, H_kv, D) -> Plan:
     if st != KF_OK:
         raise KfError(st, status_string(st))
     return Plan(PATH_NAMES[out.path], out.rows_per_group, out.num_splits, out.kv_per_split,
-                out.grid_blocks, out.block_threads, int(out.workspace_bytes))
+                out.grid_blocks, out.block_threads, int(out.workspace_bytes), out.splits_per_block)
 
 
 def workspace_bytes(B, q_len, kv_len, H_q, H_kv, D) -> int:

@@ -17,6 +17,12 @@ constexpr int kNumCUs = 256;            // MI355X compute units
 constexpr int kDecodeMaxRows = 32;      // query rows per KV head on the decode path
 constexpr int kDecodeTargetBlocks = 2 * kNumCUs;
 constexpr int kDecodeMinSplitRows = 4 * kf::kDecodeStage;  // one stage per wave
+// Short-split decode (one wave per split of 32 or 64 keys): used while the
+// job is at most kShortMaxWaves such waves (8 per CU); beyond it the work is
+// bandwidth-bound and the streaming decode kernel takes over.  64-key splits
+// are preferred while they still give kShortMinWaves waves (4 per CU).
+constexpr long long kShortMaxWaves = 8LL * kNumCUs;
+constexpr long long kShortMinWaves = 4LL * kNumCUs;
 constexpr int kMinGroupKeys = 128;      // keys before a prefill row's keys are split in two
 constexpr size_t kWsAlign = 256;
 
@@ -38,11 +44,16 @@ struct Plan {
     int threads;
     int waves;          // prefill: waves per workgroup
     int kv_groups;      // prefill: KV groups per workgroup (1 or 2)
+    int short_stages;   // decode: 32-key stages per split of the short-split kernel, 0 = streaming kernel
+    int merge_cw;       // split merge: float4 columns per wave
+    int merge_per;      // split merge: splits per lane
     size_t ws_bytes;
     size_t ws_o_off, ws_m_off, ws_l_off;
 };
 
-int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) {
+// paged: K/V come from a page pool (kf_attn_decode_paged), which only the
+// streaming decode kernel reads.
+int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl, bool paged = false) {
     if (B <= 0 || q_len <= 0 || kv_len <= 0 || H_q <= 0 || H_kv <= 0) return KF_ERR_SIZE;
     if (!supported_head_dim(D)) return KF_ERR_HEAD_DIM;
     if (H_q % H_kv != 0) return KF_ERR_GQA;
@@ -59,19 +70,45 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl) 
     p.n_groups = (int)n_groups;
     p.rows_total = (int)rows_total;
     if (R <= kDecodeMaxRows) {
-        long long splits = (kDecodeTargetBlocks + n_groups - 1) / n_groups;
-        const long long max_splits = (kv_len + kDecodeMinSplitRows - 1) / kDecodeMinSplitRows;
-        if (splits > max_splits) splits = max_splits;
-        if (splits > kf::merge_max_splits(D)) splits = kf::merge_max_splits(D);
-        if (splits < 1) splits = 1;
-        long long per = (kv_len + splits - 1) / splits;
-        per = (per + kf::kDecodeStage - 1) / kf::kDecodeStage * kf::kDecodeStage;
-        splits = (kv_len + per - 1) / per;
-        if (n_groups * splits > INT_MAX) return KF_ERR_SIZE;
+        // Short splits (one wave each) while the whole job is a few waves
+        // per CU: 64 keys per split (D <= 128) while that keeps 4 waves per
+        // CU, else 32, else 64.
+        int nst = 0;
+        if (!paged) {
+            const auto waves = [&](int st) { return n_groups * ((kv_len + 32LL * st - 1) / (32LL * st)); };
+            const auto fits = [&](int st) {
+                return st <= (D >= 256 ? 1 : 2) && waves(st) <= kShortMaxWaves &&
+                       (kv_len + 32LL * st - 1) / (32LL * st) <= kf::kMergeMaxSplits;
+            };
+            if (fits(2) && waves(2) >= kShortMinWaves) nst = 2;
+            else if (fits(1)) nst = 1;
+            else if (fits(2)) nst = 2;
+        }
+        long long splits, per;
+        if (nst > 0) {
+            per = 32LL * nst;
+            splits = (kv_len + per - 1) / per;
+            p.grid = (int)((n_groups * splits + kf::kShortWaves - 1) / kf::kShortWaves);
+            p.threads = 64 * kf::kShortWaves;
+        } else {
+            splits = (kDecodeTargetBlocks + n_groups - 1) / n_groups;
+            const long long max_splits = (kv_len + kDecodeMinSplitRows - 1) / kDecodeMinSplitRows;
+            if (splits > max_splits) splits = max_splits;
+            if (splits > kf::kMergeMaxSplits) splits = kf::kMergeMaxSplits;
+            if (splits < 1) splits = 1;
+            per = (kv_len + splits - 1) / splits;
+            per = (per + kf::kDecodeStage - 1) / kf::kDecodeStage * kf::kDecodeStage;
+            splits = (kv_len + per - 1) / per;
+            if (n_groups * splits > INT_MAX) return KF_ERR_SIZE;
+            p.grid = (int)(n_groups * splits);
+            p.threads = kf::kDecodeThreads;
+        }
+        p.short_stages = nst;
         p.n_splits = (int)splits;
         p.kv_per_split = (int)per;
-        p.grid = (int)(n_groups * splits);
-        p.threads = kf::kDecodeThreads;
+        p.merge_cw = kf::merge_cols(D, p.n_splits);
+        p.merge_per = kf::merge_per_lane(p.merge_cw, p.n_splits);
+        if (splits > 1 && rows_total * ((D / 4) / p.merge_cw) > INT_MAX) return KF_ERR_SIZE;
         p.path = splits > 1 ? KF_PATH_DECODE_SPLIT : KF_PATH_DECODE;
     } else {
         // Waves per workgroup: the most the head dimension allows.  When that
@@ -153,13 +190,31 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
         }
         return hipGetLastError();
     }
-    if (prm.block_table)
-        kf::kf_attn_decode_kernel<D, true><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
-    else
-        kf::kf_attn_decode_kernel<D, false><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+    const dim3 grid(pl.grid), block(pl.threads);
+    if (prm.block_table) {
+        kf::kf_attn_decode_kernel<D, true><<<grid, block, 0, stream>>>(prm);
+    } else if (pl.short_stages == 0) {
+        kf::kf_attn_decode_kernel<D, false><<<grid, block, 0, stream>>>(prm);
+    } else if (pl.short_stages == 1) {
+        kf::kf_attn_decode_short_kernel<D, 1><<<grid, block, 0, stream>>>(prm);
+    } else {
+        if constexpr (kf::kShortMaxStages<D> >= 2)
+            kf::kf_attn_decode_short_kernel<D, 2><<<grid, block, 0, stream>>>(prm);
+        else
+            return hipErrorInvalidValue;  // the planner never asks for it
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || pl.path != KF_PATH_DECODE_SPLIT) return e;
-    kf::kf_attn_split_merge_kernel<D><<<dim3(pl.rows_total), dim3(kf::kMergeThreads), 0, stream>>>(prm);
+    const int cw = pl.merge_cw;
+    const dim3 mgrid(pl.rows_total * ((D / 4) / cw)), mblock(kf::kMergeThreads);
+    switch (pl.merge_per) {
+        case 1: kf::kf_attn_split_merge_kernel<D, 1><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
+        case 2: kf::kf_attn_split_merge_kernel<D, 2><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
+        case 4: kf::kf_attn_split_merge_kernel<D, 4><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
+        case 8: kf::kf_attn_split_merge_kernel<D, 8><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
+        case 16: kf::kf_attn_split_merge_kernel<D, 16><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
+        default: return hipErrorInvalidValue;  // the planner caps n_splits at kMergeMaxSplits
+    }
     return hipGetLastError();
 }
 
@@ -252,6 +307,7 @@ int kf_attn_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, kf_attn
     plan->grid_blocks = pl.grid;
     plan->block_threads = pl.threads;
     plan->workspace_bytes = pl.ws_bytes;
+    plan->splits_per_block = pl.path == KF_PATH_PREFILL ? 0 : pl.short_stages > 0 ? kf::kShortWaves : 1;
     return KF_OK;
 }
 
@@ -286,7 +342,7 @@ size_t kf_attn_decode_paged_workspace_bytes(int B, int q_len, int H_q, int H_kv,
     int sh, cap;
     if (paged_geometry(page_size, max_pages_per_seq, 1, &sh, &cap) != KF_OK) return 0;
     Plan pl;
-    if (make_plan(B, q_len, cap, H_q, H_kv, D, &pl) != KF_OK || pl.path == KF_PATH_PREFILL)
+    if (make_plan(B, q_len, cap, H_q, H_kv, D, &pl, true) != KF_OK || pl.path == KF_PATH_PREFILL)
         return 0;
     return pl.ws_bytes;
 }
@@ -300,7 +356,7 @@ int kf_attn_decode_paged(const void* Q, const void* K_pages, const void* V_pages
     int st = paged_geometry(page_size, max_pages_per_seq, num_pages, &sh, &cap);
     if (st != KF_OK) return st;
     Plan pl;
-    st = make_plan(B, q_len, cap, H_q, H_kv, D, &pl);
+    st = make_plan(B, q_len, cap, H_q, H_kv, D, &pl, true);
     if (st != KF_OK) return st;
     if (pl.path == KF_PATH_PREFILL) return KF_ERR_SIZE;  // more than 32 query rows per KV head
     if (!block_table || !kv_lens) return KF_ERR_NULL;
@@ -359,6 +415,6 @@ const char* kf_status_string(int status) {
 
 int kf_last_hip_error(void) { return g_last_hip_error; }
 
-const char* kf_version(void) { return "kernelfoundry_amd 0.1.0 (gfx950)"; }
+const char* kf_version(void) { return "kernelfoundry_amd 0.2.0 (gfx950)"; }
 
 }  // extern "C"

@@ -232,8 +232,9 @@ struct StageGeom {
 
 // Register-staged loader: NT threads copy one BC-row K/V stage from HBM into
 // registers (load) and then into LDS (store), K row-major swizzled and V
-// transposed.  Rows at or beyond kv_end are zero-filled, so masked scores
-// meet zero V rows (0 * garbage could be NaN).
+// transposed.  Rows at or beyond kv_end hold row kv_end - 1 (load) or zeros
+// (load_halves, whose pages may be unallocated), so masked scores meet
+// finite V rows (0 * NaN would be NaN).
 template <int D, int BC, int NT>
 struct StageLoader {
     using G = StageGeom<D, BC>;
@@ -246,26 +247,33 @@ struct StageLoader {
     u32x4 k[kKIters];
     u32x4 v[kVIters][4];
 
+    // Unpredicated loads: rows at or beyond kv_end (kv0 < kv_end) read row
+    // kv_end - 1 instead, a valid row whose scores the caller masks to -inf
+    // (P = 0 times finite data), and lanes past the stage (idx beyond the
+    // chunk count, D = 16 V only) read chunk 0 and are never stored.  A
+    // predicated load compiles to a branch per load, and the compiler then
+    // waited for the first loads before issuing the rest.
     __device__ __forceinline__ void load(const uint16_t* __restrict__ Kh,
                                          const uint16_t* __restrict__ Vh, int kv0, int kv_end,
                                          int tid) {
+        const int last = kv_end - 1;
 #pragma unroll
         for (int i = 0; i < kKIters; ++i) {
             const int idx = tid + i * NT;
-            const bool in = (kKTotal % NT == 0) || idx < kKTotal;
-            const int row = idx / G::kChunks, c = idx % G::kChunks;
-            const int kv = kv0 + row;
-            k[i] = load16(Kh + (size_t)kv * D + c * 8, in && kv < kv_end);
+            const int idc = ((kKTotal % NT == 0) || idx < kKTotal) ? idx : 0;
+            const int row = idc / G::kChunks, c = idc % G::kChunks;
+            const int kv = min(kv0 + row, last);
+            k[i] = *reinterpret_cast<const u32x4*>(Kh + (size_t)kv * D + c * 8);
         }
 #pragma unroll
         for (int i = 0; i < kVIters; ++i) {
             const int idx = tid + i * NT;
-            const bool in = (kVTotal % NT == 0) || idx < kVTotal;
-            const int grp = idx % kVGroups, c = idx / kVGroups;
+            const int idc = ((kVTotal % NT == 0) || idx < kVTotal) ? idx : 0;
+            const int grp = idc % kVGroups, c = idc / kVGroups;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int kv = kv0 + 4 * grp + r;
-                v[i][r] = load16(Vh + (size_t)kv * D + c * 8, in && kv < kv_end);
+                const int kv = min(kv0 + 4 * grp + r, last);
+                v[i][r] = *reinterpret_cast<const u32x4*>(Vh + (size_t)kv * D + c * 8);
             }
         }
     }
@@ -336,16 +344,17 @@ struct StageLoader {
     }
 };
 
-// Q^T fragments of one wave: query row `row` of the group (zero when
-// row >= R), chunk 2*kk + (lane/32) for MFMA k-step kk.
+// Q^T fragments of one wave: query row `row` of the group, chunk
+// 2*kk + (lane/32) for MFMA k-step kk.  Lanes of rows >= R load row R - 1:
+// their score columns are computed but never stored.
 template <int D>
 __device__ __forceinline__ void load_q_frags(const uint16_t* __restrict__ Qg, int row, int R,
                                              int lane, f16x8 (&qf)[D / 16]) {
     const int g = lane >> 5;
-    const bool ok = row < R;
+    const int rc = min(row, R - 1);
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk)
-        qf[kk] = as_f16x8(load16(Qg + (size_t)row * D + (2 * kk + g) * 8, ok));
+        qf[kk] = *reinterpret_cast<const f16x8*>(Qg + (size_t)rc * D + (2 * kk + g) * 8);
 }
 
 // One 32(kv) x 32(query) block of raw scores S^T = K . Q^T.
@@ -1274,89 +1283,276 @@ void kf_attn_decode_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Split merge: one workgroup per query row.  Thread t < ns reads split t's
-// (M_t, l_t) and turns it into the weight w_t = exp(M_t - max_k M_k), staged
-// in LDS; the partial outputs are spread over kLanes groups of threads (each
-// thread owns 4 consecutive d and the splits lane + i * kLanes, i < kPre) and
-// the kLanes partial sums reduced in LDS.  Every load is issued before the
-// first reduction, so the merge costs one memory round trip.  The planner
-// never makes more splits than merge_max_splits(D) = kPre * kLanes (<= 256).
-//   O = sum_k w_k O_k / sum_k w_k l_k,  Mi = max_k M_k,  Li = sum_k w_k l_k.
+// Short-split decode: <= 32 query rows per KV head and NST * 32 keys per
+// split.  Each wave is its own (group, split), 4 waves per workgroup: at
+// entry it issues every load it needs -- the Q^T fragments, its K rows
+// straight into the MFMA A-operand layout (lane l: key row l % 32, 16-byte
+// chunk 2 kk + l / 32 for k-step kk; no LDS), and its V rows by LDS-DMA into
+// a wave-private slot (row-major, chunks XOR-swizzled by SwizzleRow<D>, read
+// back as V^T fragments with ds_read_b64_tr_b16).  All of the split's scores
+// are in registers at once, so the softmax uses their exact maximum (no
+// running rescale).  The wave writes its partial (O unnormalised, M, l) or,
+// with one split, the final row; no workgroup barrier anywhere.
 // ---------------------------------------------------------------------------
-constexpr int kMergeThreads = 256;
-constexpr int kMergePre = 4;  // partial-O vectors per thread
+constexpr int kShortWaves = 4;  // waves (independent splits) per workgroup
 
-constexpr int merge_max_splits(int D) { return kMergePre * (kMergeThreads / (D / 4)); }
+template <int D> constexpr int kShortMaxStages = D >= 256 ? 1 : 2;
 
-template <int D>
+template <int D, int NST>
+__global__ __launch_bounds__(64 * kShortWaves, D >= 256 ? 1 : 2)
+void kf_attn_decode_short_kernel(AttnParams p) {
+    static_assert(NST >= 1 && NST <= kShortMaxStages<D>, "stages per split");
+    constexpr int kRowBytes = D * 2;
+    constexpr int kChunks = D / 8;                   // 16-byte chunks per row
+    constexpr int kKeys = 32 * NST;                  // keys per split
+    constexpr int kVBytes = kKeys * kRowBytes;       // V slot per wave
+    constexpr int kRowsPerInstr = 1024 / kRowBytes;  // rows per LDS-DMA instruction
+    constexpr int kInstr = kVBytes / 1024;
+    constexpr int kNKK = D / 16;                     // MFMA k-steps over D
+    constexpr int kNTD = (D < 32 ? 32 : D) / 32;     // 32-row O^T tiles
+    static_assert(kVBytes % 1024 == 0, "V slot in whole KiB");
+    using SW = SwizzleRow<D>;
+    __shared__ __attribute__((aligned(1024))) char vbuf[kShortWaves * kVBytes];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 5;
+    const int row = lane & 31;
+    const int R = p.rows_per_group;
+    const int ns = p.n_splits;
+    const int wid = xcd_remap(blockIdx.x, gridDim.x) * kShortWaves + wave;
+    if (wid >= (p.rows_total / R) * ns) return;  // past the last split (wave-uniform)
+    const int split = wid % ns, grp = wid / ns;
+    const int kvb = batch_kv_len(p, grp);
+    const int s0 = split * kKeys;
+    const int s1 = min(kvb, s0 + kKeys);
+    const size_t ri = (size_t)grp * R + row;                  // final row index
+    const size_t pi = ((size_t)grp * ns + split) * R + row;   // partial index
+
+    if (s0 >= s1) {
+        // No key of this sequence in the split: an empty partial (or row).
+        if (row < R) {
+#pragma unroll
+            for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int d = 32 * td + 8 * i + 4 * g;
+                    if (d < D) {
+                        if (ns == 1)
+                            store_out4(p, ri * D + d, f32x4{0.f, 0.f, 0.f, 0.f});
+                        else
+                            *reinterpret_cast<f32x4*>(p.Opart + pi * D + d) = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+                }
+            if (g == 0) {
+                if (ns == 1) {
+                    store_stats(p, ri, -INFINITY, 0.f);
+                } else {
+                    p.Mpart[pi] = -INFINITY;
+                    p.Lpart[pi] = 0.f;
+                }
+            }
+        }
+        return;
+    }
+
+    // ---- Loads, all issued before the first wait (one memory round trip):
+    // V into LDS, then the Q^T fragments and K into registers.  All are
+    // unpredicated: rows past s1 re-read row s1 - 1, whose scores are masked
+    // below. ----
+    const int last = s1 - 1;
+    const uint16_t* Qg = p.Q + (size_t)grp * R * D;
+    const uint16_t* Kh = p.K + (size_t)grp * p.kv_len * D;
+    const char* Vh = reinterpret_cast<const char*>(p.V + (size_t)grp * p.kv_len * D);
+    // Lane l of DMA instruction ii writes LDS bytes [16 l, 16 l + 16) of KiB ii
+    // of the slot: row r = ii * kRowsPerInstr + l / kChunks, physical chunk
+    // l % kChunks, which holds logical chunk (l % kChunks) ^ h(r) of key s0 + r.
+    char* const vs = vbuf + wave * kVBytes;
+#pragma unroll
+    for (int ii = 0; ii < kInstr; ++ii) {
+        const int r = ii * kRowsPerInstr + lane / kChunks;
+        const int kv = min(s0 + r, last);
+        const uint32_t off = (uint32_t)kv * kRowBytes +
+                             (uint32_t)((((lane % kChunks) ^ SW::h(r)) % kChunks) * 16);
+        __builtin_amdgcn_global_load_lds(Vh + off, (lds_void*)(vs + ii * 1024), 16, 0, 0);
+    }
+    f16x8 qf[kNKK];
+    load_q_frags<D>(Qg, row, R, lane, qf);
+    f16x8 kf[NST][kNKK];
+#pragma unroll
+    for (int b = 0; b < NST; ++b) {
+        const int kv = min(s0 + 32 * b + row, last);
+#pragma unroll
+        for (int kk = 0; kk < kNKK; ++kk)
+            kf[b][kk] = *reinterpret_cast<const f16x8*>(Kh + (size_t)kv * D + (2 * kk + g) * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // no MFMA (and its wait) above the loads
+
+    // ---- Scores S^T = K Q^T (kv x query row), masked past each row's keys. ----
+    f32x16 s[NST];
+#pragma unroll
+    for (int b = 0; b < NST; ++b) {
+        s[b] = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < kNKK; ++kk) s[b] = mfma32(kf[b][kk], qf[kk], s[b]);
+    }
+    const int lim_min = p.causal ? max(kvb - p.q_len + 1, 0) : kvb;  // keys every row sees
+    if (s0 + kKeys > min(s1, lim_min)) {
+        const int lim_lane = row < R ? row_kv_limit(p, kvb, row % p.q_len) : kvb;
+        block_mask<NST>(s, min(s1, lim_lane) - s0, lane);
+    }
+
+    // ---- Softmax against the exact row max; fp16 P^T fragments. ----
+    const float mx = block_rowmax<NST>(s);  // raw scores; shared with lane l ^ 32
+    const bool empty = mx == -INFINITY;     // no visible key for this row
+    const float neg_m = empty ? 0.f : -mx * p.scale_log2;
+    f16x8 pp[2 * NST];
+    float lsum = 0.f;
+#pragma unroll
+    for (int b = 0; b < NST; ++b) lsum += block_exp(s[b], p.scale_log2, neg_m, pp[2 * b], pp[2 * b + 1]);
+    const float l = lsum + __shfl_xor(lsum, 32);
+
+    // ---- O^T = V^T P^T; V^T fragments by ds_read_b64_tr_b16 from the slot. ----
+    // 16-lane group G = l / 16, w = l % 16 supplies key row 4 (G / 2) + w / 4
+    // (+8 for the second half of the 16-key step) and the 8 bytes at
+    // d = 32 td + 16 (G % 2) + 4 (w % 4).  D = 16: groups with d >= 16 give
+    // the zero rows 16..31 of V^T (their reads, of valid rows, are discarded).
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot's LDS-DMA has landed
+    const int G = lane >> 4, w = lane & 15;
+    f32x16 o[kNTD];
+#pragma unroll
+    for (int td = 0; td < kNTD; ++td) {
+        o[td] = f32x16{};
+        const int d = 32 * td + 16 * (G & 1) + 4 * (w & 3);
+        const bool dok = d < D;
+        const int dc = dok ? d : d - 16;
+        int voff[2];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const int r = 4 * (G >> 1) + (w >> 2) + 8 * h2;
+            voff[h2] = r * kRowBytes + (((dc >> 3) ^ SW::h(r)) % kChunks) * 16 + ((dc >> 2) & 1) * 8;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 2 * NST; ++jj) {
+            const f16x4 lo = lds_read_tr16(vs + voff[0] + jj * 16 * kRowBytes);
+            const f16x4 hi = lds_read_tr16(vs + voff[1] + jj * 16 * kRowBytes);
+            f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            if (D < 32 && !dok) a = f16x8{};
+            o[td] = mfma32(a, pp[jj], o[td]);
+        }
+    }
+
+    // ---- Output: this split's partial, or the final row with one split. ----
+    if (row < R) {
+        const float inv = empty ? 0.f : 1.0f / l;
+#pragma unroll
+        for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 32 * td + 8 * i + 4 * g;
+                if (d < D) {
+                    const f32x4 v = {o[td][4 * i], o[td][4 * i + 1], o[td][4 * i + 2], o[td][4 * i + 3]};
+                    if (ns == 1)
+                        store_out4(p, ri * D + d, v * inv);
+                    else
+                        *reinterpret_cast<f32x4*>(p.Opart + pi * D + d) = v;
+                }
+            }
+        if (g == 0) {
+            const float m_nat = empty ? -INFINITY : mx * p.scale;
+            if (ns == 1) {
+                store_stats(p, ri, m_nat, empty ? 0.f : l);
+            } else {
+                p.Mpart[pi] = m_nat;
+                p.Lpart[pi] = empty ? 0.f : l;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Split merge: one wave per (query row, block of CW float4 columns of O);
+// CW is a power of two in [4, D/4] chosen by the host.  Lane l owns column
+// c = cb * CW + l % CW and the splits k = l / CW + i * (64 / CW), i < NPER
+// (NPER, a power of two <= kMergePer, covers n_splits).  Every load (partial
+// O, M, l) is unconditional and issued before the first use, so the merge
+// costs one memory round trip; the reductions over the 64 / CW lanes of a
+// column are in-wave shuffles (no LDS, no barrier).  Every wave of a row
+// computes the row's max and l itself.  The planner never makes more splits
+// than kMergeMaxSplits = kMergePer * 16.
+//   O = sum_k w_k O_k / sum_k w_k l_k,  w_k = exp(M_k - max_j M_j),
+//   Mi = max_k M_k,  Li = sum_k w_k l_k.
+// ---------------------------------------------------------------------------
+constexpr int kMergeThreads = 64;
+constexpr int kMergePer = 16;                  // most splits per lane
+constexpr int kMergeMaxSplits = kMergePer * 16;  // CW = 4: 16 split lanes
+
+// Float4 columns per merge wave for ns splits: the widest block whose
+// 64 / CW split lanes cover ns with at most kMergePer splits each.
+constexpr int merge_cols(int D, int ns) {
+    int cw = D / 4 < 64 ? D / 4 : 64;
+    while (cw > 4 && (ns + 64 / cw - 1) / (64 / cw) > kMergePer) cw /= 2;
+    return cw;
+}
+
+// Splits per lane (a power of two) for ns splits over 64 / cw split lanes.
+constexpr int merge_per_lane(int cw, int ns) {
+    const int need = (ns + 64 / cw - 1) / (64 / cw);
+    int per = 1;
+    while (per < need) per *= 2;
+    return per;
+}
+
+template <int D, int NPER>
 __global__ __launch_bounds__(kMergeThreads)
-void kf_attn_split_merge_kernel(AttnParams p) {
-    constexpr int kD4 = D / 4;                     // float4 columns per row
-    constexpr int kLanes = kMergeThreads / kD4;    // split lanes
-    constexpr int kPre = kMergePre;
-    static_assert(merge_max_splits(D) <= kMergeThreads, "one split per thread in phase 1");
-    __shared__ float s_w[kMergeThreads];
-    __shared__ float s_red[kMergeThreads / 64];
-    __shared__ f32x4 s_acc[kLanes][kD4];
-
-    const int tid = threadIdx.x;
-    const int row = blockIdx.x;                    // global query row
+void kf_attn_split_merge_kernel(AttnParams p, int cw) {
+    static_assert(NPER >= 1 && NPER <= kMergePer, "splits per lane");
+    const int lane = threadIdx.x;
+    const int ncb = (D / 4) / cw;                  // column blocks per row
+    const int row = blockIdx.x / ncb;              // global query row
+    const int cb = blockIdx.x % ncb;
     const int R = p.rows_per_group;
     const int grp = row / R, r = row % R;
-    const int ns = p.n_splits;                     // <= merge_max_splits(D)
+    const int ns = p.n_splits;                     // 1 .. NPER * 64 / cw
+    const int sl_n = 64 / cw;                      // split lanes per column
     const size_t base = (size_t)grp * ns * R + r;  // partial index of split 0
-    const int lane = tid / kD4, d4 = tid % kD4;
-    const float* Ob = p.Opart + base * D + 4 * d4;
+    const int c = cb * cw + (lane & (cw - 1)), sl = lane / cw;
 
-    f32x4 opre[kPre];
+    f32x4 o[NPER];
+    float mk[NPER], lk[NPER];
 #pragma unroll
-    for (int i = 0; i < kPre; ++i) {
-        const int k = lane + i * kLanes;
-        opre[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (k < ns) opre[i] = *reinterpret_cast<const f32x4*>(Ob + (size_t)k * R * D);
+    for (int i = 0; i < NPER; ++i) {
+        // Splits past ns read split ns - 1 and get weight 0 below.
+        const size_t pi = base + (size_t)min(sl + i * sl_n, ns - 1) * R;
+        o[i] = *reinterpret_cast<const f32x4*>(p.Opart + pi * D + 4 * c);
+        mk[i] = p.Mpart[pi];
+        lk[i] = p.Lpart[pi];
     }
-    float m0 = -INFINITY, l0 = 0.f;
-    if (tid < ns) {
-        m0 = p.Mpart[base + (size_t)tid * R];
-        l0 = p.Lpart[base + (size_t)tid * R];
-    }
-
-    // Max over splits, weights, l = sum w_k l_k.
-    float m = m0;
+    float m = -INFINITY;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if ((tid & 63) == 0) s_red[tid >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    for (int i = 0; i < NPER; ++i)
+        if (sl + i * sl_n < ns) m = fmaxf(m, mk[i]);
+    for (int off = cw; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
     const bool none = m == -INFINITY;  // no split saw a key for this row
-    float lsum = 0.f;
-    if (tid < ns) {
-        const float w = none ? 0.f : exp2_hw((m0 - m) * kLog2e);
-        s_w[tid] = w;
-        lsum = w * l0;
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off);
-    __syncthreads();  // s_red reuse; s_w complete
-    if ((tid & 63) == 0) s_red[tid >> 6] = lsum;
-    __syncthreads();
-    const float l = s_red[0] + s_red[1] + s_red[2] + s_red[3];
-
-    // Weighted sum of the partial outputs.
+    float l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < kPre; ++i) {
-        const int k = lane + i * kLanes;
-        if (k < ns) acc += s_w[k] * opre[i];
+    for (int i = 0; i < NPER; ++i) {
+        const bool live = sl + i * sl_n < ns && !none;
+        const float w = live ? exp2_hw((mk[i] - m) * kLog2e) : 0.f;
+        l += w * lk[i];
+        acc += w * o[i];
     }
-    s_acc[lane][d4] = acc;
-    __syncthreads();
-    if (tid < kD4) {
-        f32x4 t = s_acc[0][tid];
-#pragma unroll
-        for (int j = 1; j < kLanes; ++j) t += s_acc[j][tid];
-        store_out4(p, (size_t)row * D + 4 * tid, t * (l > 0.f ? 1.0f / l : 0.f));
-        if (tid == 0) store_stats(p, row, m, l);
+    for (int off = cw; off < 64; off <<= 1) {
+        l += __shfl_xor(l, off);
+        acc.x += __shfl_xor(acc.x, off);
+        acc.y += __shfl_xor(acc.y, off);
+        acc.z += __shfl_xor(acc.z, off);
+        acc.w += __shfl_xor(acc.w, off);
+    }
+    if (sl == 0) {
+        store_out4(p, (size_t)row * D + 4 * c, acc * (l > 0.f ? 1.0f / l : 0.f));
+        if (c == 0) store_stats(p, row, m, l);
     }
 }
 

@@ -146,14 +146,19 @@ def test_plans_for_baseline_configs():
     assert p.path == "prefill" and p.block_threads == 256  # 2 row waves x 2 KV groups
     assert p.grid_blocks == 8 * (4 * 512 // 64) == 256
     assert p.workspace_bytes == 0
-    p = kf.plan(1, 1, 4096, 32, 8, 128)              # C2 decode
+    assert p.splits_per_block == 0
+    p = kf.plan(1, 1, 4096, 32, 8, 128)              # C2 decode: 1024 one-wave splits
     assert p.path == "decode_split" and p.rows_per_group == 4
+    assert p.splits_per_block == 4 and p.kv_per_split == 32 and p.num_splits == 128
+    assert p.grid_blocks == 8 * 128 // 4 and p.block_threads == 256
     p = kf.plan(1, 2048, 2048, 32, 1, 64)            # C4a MQA prefill
     assert p.path == "prefill" and p.rows_per_group == 32 * 2048
     p = kf.plan(1, 1, 2048, 32, 1, 64)               # C4b MQA decode
     assert p.path == "decode_split" and p.rows_per_group == 32
-    p = kf.plan(32, 1, 8192, 32, 8, 128)             # C5 batched decode
+    assert p.splits_per_block == 4 and p.num_splits == 64 and p.grid_blocks == 16
+    p = kf.plan(32, 1, 8192, 32, 8, 128)             # C5 batched decode: streaming kernel
     assert p.path == "decode_split" and p.grid_blocks == 256 * p.num_splits
+    assert p.splits_per_block == 1 and p.num_splits == 2
 
 
 @pytest.mark.parametrize("B,q,kv,H_q,H_kv,D", [
@@ -165,25 +170,37 @@ def test_decode_split_geometry_covers_kv(B, q, kv, H_q, H_kv, D):
     assert p.rows_per_group == (H_q // H_kv) * q <= 32
     assert p.kv_per_split % 32 == 0
     assert (p.num_splits - 1) * p.kv_per_split < kv <= p.num_splits * p.kv_per_split
-    assert p.grid_blocks == B * H_kv * p.num_splits
+    splits = B * H_kv * p.num_splits
+    if p.splits_per_block == 4:
+        # Short-split kernel: one wave per split of 32 or 64 keys (64 only for
+        # D <= 128), 4 per workgroup, at most 8 waves per CU.
+        assert p.kv_per_split in ((32, 64) if D <= 128 else (32,))
+        assert p.grid_blocks == -(-splits // 4) and p.block_threads == 256 and splits <= 2048
+    else:
+        assert p.splits_per_block == 1 and p.grid_blocks == splits and p.block_threads == 256
+        assert p.kv_per_split >= 128 or p.num_splits == 1
     if p.num_splits == 1:
         assert p.path == "decode" and p.workspace_bytes == 0
     else:
         parts = B * H_q * q * p.num_splits
         assert p.workspace_bytes >= parts * (D + 2) * 4
-        # The split merge reads every partial in one pass: 4 per thread.
-        assert p.num_splits <= 4 * (256 // (D // 4))
+        # The split merge reads every partial in one pass.
+        assert p.num_splits <= 256
 
 
-@pytest.mark.parametrize("B,H_kv,kv,D,splits", [
-    (1, 8, 131072, 128, 32), (1, 1, 262144, 128, 32), (1, 1, 65536, 64, 64),
-    (1, 1, 1 << 20, 16, 256), (1, 4, 40000, 256, 16), (1, 8, 8192, 128, 32),
+@pytest.mark.parametrize("B,H_kv,kv,D,splits,per_block", [
+    (1, 8, 131072, 128, 64, 1), (1, 1, 262144, 128, 256, 1), (1, 1, 65536, 64, 256, 1),
+    (1, 1, 1 << 20, 16, 256, 1), (1, 4, 40000, 256, 125, 1), (1, 8, 8192, 128, 128, 4),
+    (1, 8, 4096, 128, 128, 4), (1, 8, 16384, 128, 256, 4), (2, 8, 16384, 128, 32, 1),
 ])
-def test_decode_splits_capped_at_merge_capacity(B, H_kv, kv, D, splits):
-    """Few KV groups over a long KV want more splits than the merge kernel
-    reads in one pass; the plan stops at that capacity (4096 / D splits)."""
+def test_decode_split_counts(B, H_kv, kv, D, splits, per_block):
+    """Streaming decode: splits target 2 workgroups per CU, at most the 256
+    partials the split merge reads in one pass.  Short-split decode: 64-key
+    splits while they give 4 waves per CU, else 32-key ones, up to 8 waves
+    per CU and 256 splits."""
     p = kf.plan(B, 1, kv, 32, H_kv, D)
     assert p.path == "decode_split" and p.num_splits == splits
+    assert p.splits_per_block == per_block
     assert p.num_splits * p.kv_per_split >= kv
 
 
@@ -258,7 +275,11 @@ def test_paged_decode_validation():
     assert _paged(flags=16) == kf.KF_ERR_FLAGS
     assert _paged(flags=kf.KF_ATTN_OUT_F16 | kf.KF_ATTN_OUT_BF16) == kf.KF_ERR_FLAGS
     need = kf.paged_workspace_bytes(2, 1, 32, 8, 128, 16, 64)
-    assert need == kf.workspace_bytes(2, 1, 64 * 16, 32, 8, 128) > 0
+    # Paged decode always runs the streaming kernel: 8 splits of 128 keys over
+    # the 1024-key capacity, each a partial of 2 x 32 rows of D + 2 floats (the
+    # same shape unpaged runs 32-key one-wave splits).
+    assert need == 8 * 64 * (128 + 2) * 4
+    assert kf.workspace_bytes(2, 1, 64 * 16, 32, 8, 128) == 32 * 64 * (128 + 2) * 4
     assert _paged(ws_bytes=need - 1) == kf.KF_ERR_WORKSPACE
     assert kf.paged_workspace_bytes(2, 9, 32, 8, 128, 16, 64) == 0    # not a decode shape
     assert kf.paged_workspace_bytes(2, 1, 32, 8, 128, 24, 64) == 0    # bad page size

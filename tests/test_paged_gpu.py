@@ -113,17 +113,20 @@ def test_paged_decode_parity(case):
 def test_paged_in_order_equals_contiguous_bitwise(page_size):
     """Pages holding the rows of a contiguous cache in order: the paged kernel
     computes exactly what kf_attn_fwd_ex computes on the contiguous cache
-    (same splits, same stages, same arithmetic)."""
+    (same splits, same stages, same arithmetic).  The batch is large enough
+    for the contiguous plan to use the streaming decode kernel too (paged
+    decode always does)."""
     import kernelfoundry_amd as kf
     torch = _torch()
-    B, H_q, H_kv, D, max_pages = 2, 32, 8, 128, 4096 // page_size
+    B, H_q, H_kv, D, max_pages = 12, 32, 8, 128, 4096 // page_size
     cap = max_pages * page_size
+    assert kf.plan(B, 1, cap, H_q, H_kv, D).splits_per_block == 1
     _announce(test="paged_vs_contiguous", page_size=page_size)
     q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 1, cap, D, 314)
     to_pages = lambda a: a.reshape(B, H_kv, max_pages, page_size, D).transpose(0, 2, 1, 3, 4) \
         .reshape(B * max_pages, H_kv, page_size, D)
     table = np.arange(B * max_pages, dtype=np.int32).reshape(B, max_pages)
-    lens = np.array([cap, cap - 100], dtype=np.int32)
+    lens = np.array([cap - 37 * b for b in range(B)], dtype=np.int32)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     Op = kf.attn_decode_paged(t(q16), t(to_pages(k16)), t(to_pages(v16)), t(table), t(lens))
     Oc = kf.attn_fwd(t(q16), t(k16), t(v16), kv_lens=t(lens))

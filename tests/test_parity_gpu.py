@@ -232,15 +232,16 @@ def test_config_c5_batched_long_decode():
     _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (7, 9), (31, 31), (16, 4)])
 
 
-@pytest.mark.parametrize("H_q,H_kv,kv", [(32, 8, 131072), (32, 1, 262144)])
-def test_long_context_decode(H_q, H_kv, kv):
+@pytest.mark.parametrize("H_q,H_kv,kv,splits", [(32, 8, 131072, 64), (32, 1, 262144, 256)])
+def test_long_context_decode(H_q, H_kv, kv, splits):
     """One sequence of 128 K / 256 K keys (GQA and MQA with 32 query rows per
-    KV head): the split count stops at the merge kernel's one-pass capacity;
+    KV head) on the streaming decode kernel: 2 workgroups per CU, the MQA
+    case stopping at the merge kernel's one-pass capacity of 256 splits;
     sampled heads against the oracle plus properties."""
     import kernelfoundry_amd as kf
     B, D = 1, 128
     pl = kf.plan(B, 1, kv, H_q, H_kv, D)
-    assert pl.path == "decode_split" and pl.num_splits == 32
+    assert pl.path == "decode_split" and pl.num_splits == splits and pl.splits_per_block == 1
     _announce(test="long_decode", H_q=H_q, H_kv=H_kv, kv=kv, splits=pl.num_splits)
     q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 1, kv, D, 9000 + H_kv)
     O, Mi, Li = _run_kf(q16, k16, v16)
@@ -248,15 +249,17 @@ def test_long_context_decode(H_q, H_kv, kv):
     _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (0, H_q - 1)])
 
 
-def test_split_merge_needs_no_workspace_init():
+@pytest.mark.parametrize("B,per_block", [(2, 4), (16, 1)])
+def test_split_merge_needs_no_workspace_init(B, per_block):
     """Split partials live in the caller's workspace: a workspace full of
     garbage, and one reused across calls, must both give the oracle's answer
-    (every partial is written before the merge reads it)."""
+    (every partial is written before the merge reads it), from the
+    short-split kernel (B = 2) and the streaming one (B = 16)."""
     import kernelfoundry_amd as kf
     torch = _torch()
-    B, H_q, H_kv, kv_len, D = 2, 16, 4, 2500, 128
+    H_q, H_kv, kv_len, D = 16, 4, 2500, 128
     pl = kf.plan(B, 1, kv_len, H_q, H_kv, D)
-    assert pl.path == "decode_split" and pl.num_splits > 1
+    assert pl.path == "decode_split" and pl.num_splits > 1 and pl.splits_per_block == per_block
     _announce(test="split_ws_garbage", B=B, kv_len=kv_len, splits=pl.num_splits)
     q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 1, kv_len, D, 61)
     Or, Mr, Lr = orc.sdpa(q16, k16, v16)

@@ -1,11 +1,12 @@
 """Seeded random-shape parity sweep of kf_attn_fwd_ex on the GPU.
 
 Shapes, masks and output formats are drawn from a fixed seed so that, taken
-together, they cross every dispatch the planner makes: the decode kernel with
-and without the split merge, and the prefill kernel in every workgroup
-layout (8 waves x 256 rows, two KV groups of 8 or 4 waves, 4 and 2 waves;
-D = 256 with 4 waves), with causal masking, per-sequence key counts (empty
-sequences included), ragged lengths and every head dimension.  Each case is
+together, they cross every dispatch the planner makes: the short-split decode
+kernel (32- and 64-key splits) and the streaming decode kernel, each with and
+without the split merge, and the prefill kernel in every workgroup layout
+(8 waves x 256 rows, two KV groups of 8 or 4 waves, 4 and 2 waves; D = 256
+with 4 waves), with causal masking, per-sequence key counts (empty sequences
+included), ragged lengths and every head dimension.  Each case is
 compared with oracle/attn_oracle.py's fp64 ``sdpa`` on the same fp16 inputs at
 the north-star bar (max |got - ref| <= 2e-3, ||got - ref|| / ||ref|| <= 1e-2;
 Mi to 1e-4, Li to 1e-3 relative; rows without keys exactly O = 0, Mi = -inf,
@@ -43,9 +44,17 @@ def _cases(n=40, seed=2026):
                 kv_lens = [min(x, kv_len) for x in kv_lens]
         out.append((B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens, int(rng.integers(1 << 30))))
     # Layouts random small shapes rarely reach: decode without split (at most
-    # 128 keys) and 8-wave workgroups (a grid of >= 256 workgroups x 256 rows).
-    out.append((3, 8, 8, 1, 100, 128, True, [100, 0, 37], 11))
+    # 32 keys), 8-wave workgroups (a grid of >= 256 workgroups x 256 rows),
+    # the streaming decode kernel (more than 2048 short splits) with and
+    # without the merge, 64-key short splits and a merge over 256 splits.
+    out.append((3, 8, 8, 1, 30, 128, True, [30, 0, 17], 11))
     out.append((2, 64, 8, 1024, 200, 64, True, [200, 150], 12))
+    out.append((16, 32, 8, 1, 1100, 128, False, None, 13))
+    out.append((24, 8, 8, 1, 1500, 64, True, [int(x) for x in rng.integers(0, 1501, size=24)], 14))
+    out.append((300, 8, 8, 1, 100, 16, False, None, 15))
+    out.append((32, 8, 8, 1, 200, 16, True, [int(x) for x in rng.integers(0, 201, size=32)], 16))
+    out.append((1, 4, 2, 1, 8192, 128, False, None, 17))
+    out.append((1, 4, 2, 1, 300, 256, True, [257], 18))
     return out
 
 
@@ -53,12 +62,13 @@ CASES = _cases()
 
 
 def _layout(kf, B, H_q, H_kv, q_len, kv_len, D):
-    """(path,) for decode; ("prefill", waves, kv_groups) for prefill, where
-    kv_groups follows from the grid: two KV groups put 16 * waves query rows
-    in a workgroup, one group 32 * waves."""
+    """(path, kernel) for decode, kernel "short32" / "short64" (one wave per
+    split of that many keys) or "stream"; ("prefill", waves, kv_groups) for
+    prefill, where kv_groups follows from the grid: two KV groups put
+    16 * waves query rows in a workgroup, one group 32 * waves."""
     p = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
     if p.path != "prefill":
-        return (p.path,)
+        return (p.path, f"short{p.kv_per_split}" if p.splits_per_block == 4 else "stream")
     waves = p.block_threads // 64
     R = H_q // H_kv * q_len
     groups = 2 if p.grid_blocks == B * H_kv * -(-R // (16 * waves)) and waves >= 4 and D <= 128 else 1
@@ -69,9 +79,13 @@ def test_sweep_covers_every_dispatch():
     """The drawn cases reach every kernel layout the planner chooses."""
     import kernelfoundry_amd as kf
     seen = {_layout(kf, *c[:6]) for c in CASES}
-    want = {("decode",), ("decode_split",), ("prefill", 8, 1), ("prefill", 8, 2),
-            ("prefill", 4, 2), ("prefill", 4, 1), ("prefill", 2, 1)}
+    want = {("decode", "short32"), ("decode_split", "short32"), ("decode_split", "short64"),
+            ("decode", "stream"), ("decode_split", "stream"),
+            ("prefill", 8, 1), ("prefill", 8, 2), ("prefill", 4, 2), ("prefill", 4, 1),
+            ("prefill", 2, 1)}
     assert want <= seen, sorted(seen)
+    # The split merge at its widest: 256 partials per row (4 columns per wave).
+    assert any(kf.plan(c[0], c[3], c[4], c[1], c[2], c[5]).num_splits == 256 for c in CASES)
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_q{}_kv{}_D{}_c{}_{}".format(
