@@ -205,15 +205,45 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || pl.path != KF_PATH_DECODE_SPLIT) return e;
-    const int cw = pl.merge_cw;
-    const dim3 mgrid(pl.rows_total * ((D / 4) / cw)), mblock(kf::kMergeThreads);
-    switch (pl.merge_per) {
-        case 1: kf::kf_attn_split_merge_kernel<D, 1><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
-        case 2: kf::kf_attn_split_merge_kernel<D, 2><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
-        case 4: kf::kf_attn_split_merge_kernel<D, 4><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
-        case 8: kf::kf_attn_split_merge_kernel<D, 8><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
-        case 16: kf::kf_attn_split_merge_kernel<D, 16><<<mgrid, mblock, 0, stream>>>(prm, cw); break;
-        default: return hipErrorInvalidValue;  // the planner caps n_splits at kMergeMaxSplits
+    const dim3 mgrid(pl.rows_total * ((D / 4) / pl.merge_cw)), mblock(kf::kMergeThreads);
+    constexpr int kCWMax = D / 4 < 64 ? D / 4 : 64;
+    if (pl.merge_cw == kCWMax) {
+        switch (pl.merge_per) {
+            case 1: kf::kf_attn_split_merge_kernel<D, 1, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
+            case 2: kf::kf_attn_split_merge_kernel<D, 2, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
+            case 4: kf::kf_attn_split_merge_kernel<D, 4, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
+            case 8: kf::kf_attn_split_merge_kernel<D, 8, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
+            case 16: kf::kf_attn_split_merge_kernel<D, 16, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
+            default: return hipErrorInvalidValue;  // the planner caps n_splits at kMergeMaxSplits
+        }
+    } else {
+        // Narrower column blocks are only planned with kMergePer splits per lane.
+        if (pl.merge_per != kf::kMergePer) return hipErrorInvalidValue;
+        switch (pl.merge_cw) {
+            case 4: kf::kf_attn_split_merge_kernel<D, kf::kMergePer, 4><<<mgrid, mblock, 0, stream>>>(prm); break;
+            case 8:
+                if constexpr (kCWMax > 8) {
+                    kf::kf_attn_split_merge_kernel<D, kf::kMergePer, 8><<<mgrid, mblock, 0, stream>>>(prm);
+                    break;
+                } else {
+                    return hipErrorInvalidValue;
+                }
+            case 16:
+                if constexpr (kCWMax > 16) {
+                    kf::kf_attn_split_merge_kernel<D, kf::kMergePer, 16><<<mgrid, mblock, 0, stream>>>(prm);
+                    break;
+                } else {
+                    return hipErrorInvalidValue;
+                }
+            case 32:
+                if constexpr (kCWMax > 32) {
+                    kf::kf_attn_split_merge_kernel<D, kf::kMergePer, 32><<<mgrid, mblock, 0, stream>>>(prm);
+                    break;
+                } else {
+                    return hipErrorInvalidValue;
+                }
+            default: return hipErrorInvalidValue;
+        }
     }
     return hipGetLastError();
 }

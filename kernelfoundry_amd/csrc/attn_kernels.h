@@ -49,6 +49,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 namespace kf {
@@ -122,12 +124,13 @@ __device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
-// Store the 4 consecutive output elements O[e .. e+3] in p.out_dtype
-// (e is a multiple of 4; O is 16-byte aligned).
-__device__ __forceinline__ void store_out4(const AttnParams& p, size_t e, const f32x4& v) {
-    if (p.out_dtype == kOutF32) {
+// Store the 4 consecutive output elements O[e .. e+3] as kOut (e is a
+// multiple of 4; O is 16-byte aligned).
+template <int kOut>
+__device__ __forceinline__ void store_out4_as(const AttnParams& p, size_t e, const f32x4& v) {
+    if constexpr (kOut == kOutF32) {
         *reinterpret_cast<f32x4*>(p.O + e) = v;
-    } else if (p.out_dtype == kOutF16) {
+    } else if constexpr (kOut == kOutF16) {
         const f16x4 h = __builtin_convertvector(v, f16x4);
         *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(p.O) + e) = h;
     } else {
@@ -136,6 +139,32 @@ __device__ __forceinline__ void store_out4(const AttnParams& p, size_t e, const 
         w.y = bf16_rne_bits(v[2]) | (bf16_rne_bits(v[3]) << 16);
         *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.O) + e) = w;
     }
+}
+
+// The same in p.out_dtype.
+__device__ __forceinline__ void store_out4(const AttnParams& p, size_t e, const f32x4& v) {
+    if (p.out_dtype == kOutF32)
+        store_out4_as<kOutF32>(p, e, v);
+    else if (p.out_dtype == kOutF16)
+        store_out4_as<kOutF16>(p, e, v);
+    else
+        store_out4_as<kOutBF16>(p, e, v);
+}
+
+// Row `ri` of O from the O^T accumulator tiles of one lane (d = 32 td + 8 i +
+// 4 g .. +3 in o[td][4 i .. 4 i + 3]), scaled by inv, as kOut.
+template <int kOut, int D, int NTD>
+__device__ __forceinline__ void store_o_row(const AttnParams& p, size_t ri, const f32x16 (&o)[NTD],
+                                            float inv, int g) {
+#pragma unroll
+    for (int td = 0; td < NTD; ++td)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = 32 * td + 8 * i + 4 * g;
+            if (d < D)
+                store_out4_as<kOut>(p, ri * D + d, f32x4{o[td][4 * i] * inv, o[td][4 * i + 1] * inv,
+                                                         o[td][4 * i + 2] * inv, o[td][4 * i + 3] * inv});
+        }
 }
 
 // Row statistics of query row r: Mi and Li, or LSE = Mi + ln(Li) (-inf for a
@@ -183,6 +212,44 @@ __device__ __forceinline__ f32x16 mfma32(const f16x8& a, const f16x8& b, const f
 }
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane reductions on the VALU (no LDS round trip, unlike ds_bpermute):
+// v_permlane32_swap(x, x) yields the lower half's values in both halves and
+// the upper half's values in both halves, v_permlane16_swap the same for the
+// even and odd 16-lane rows, and DPP row_ror:n rotates each 16-lane row by n.
+// Every lane receives the result; max and + are commutative, so the lanes of
+// a pair compute bit-identical values.
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Reduce v over the lanes that agree with this one modulo CW (a power of two
+// <= 64): the offsets CW, 2 CW, ..., 32.
+template <int CW, bool kMax>
+__device__ __forceinline__ float reduce_mod(float v) {
+    static_assert(CW >= 1 && CW <= 64 && (CW & (CW - 1)) == 0, "power of two");
+    auto op = [](float a, float b) { return kMax ? fmaxf(a, b) : a + b; };
+    auto ror = [](float x, auto ctrl) {  // DPP row_ror:n has control 0x120 + n
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    if constexpr (CW <= 1) v = op(v, ror(v, std::integral_constant<int, 0x121>{}));
+    if constexpr (CW <= 2) v = op(v, ror(v, std::integral_constant<int, 0x122>{}));
+    if constexpr (CW <= 4) v = op(v, ror(v, std::integral_constant<int, 0x124>{}));
+    if constexpr (CW <= 8) v = op(v, ror(v, std::integral_constant<int, 0x128>{}));
+    if constexpr (CW <= 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    if constexpr (CW <= 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    return v;
+}
 
 __device__ __forceinline__ u32x4 load16(const uint16_t* p, bool pred) {
     u32x4 v = {0u, 0u, 0u, 0u};
@@ -403,7 +470,7 @@ __device__ __forceinline__ void softmax_update(f32x16 (&s)[NSB], RowState& st,
     for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = max_xor32(mx);
     st.rmax = fmaxf(st.rmax, mx);
     const float mt = mx * scale_log2;
     const bool need = mt > st.m + kLazyRescaleLog2;
@@ -565,7 +632,7 @@ __device__ __forceinline__ float block_rowmax(const f32x16 (&s)[NSB]) {
     for (int b = 0; b < NSB; ++b)
 #pragma unroll
         for (int r = (b == 0 ? 2 : 0); r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-    return fmaxf(mx, __shfl_xor(mx, 32));
+    return max_xor32(mx);
 }
 
 template <int NSB>
@@ -993,7 +1060,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
         constexpr int kSlots = (KS - 1) * kRowWaves;
         static_assert(kSlotFloats * 4 <= S::kStageBytes && kSlots <= 3 * KS, "merge slots");
         __shared__ float merge_ml[2 * kSlots * 64];
-        const float l_pair = st.l + __shfl_xor(st.l, 32);
+        const float l_pair = sum_xor32(st.l);
         const bool none = st.rmax == -INFINITY;
         const float m_g = none ? -INFINITY : st.rmax * p.scale;
         const float beta = none ? 0.f : exp2_hw(st.m - st.rmax * p.scale_log2);
@@ -1053,7 +1120,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     }
 
     // ---- Epilogue: combine the two half-row partial sums, normalise, store. ----
-    const float l = st.l + __shfl_xor(st.l, 32);
+    const float l = sum_xor32(st.l);
     const bool empty = kMask && !(l > 0.f);  // no visible key
     if (row < R) {
         const float inv = empty ? 0.f : 1.0f / l;
@@ -1208,7 +1275,7 @@ void kf_attn_decode_kernel(AttnParams p) {
     }
 
     // Rebase this wave's state onto its true max (natural-log scaled units).
-    const float l_pair = st.l + __shfl_xor(st.l, 32);
+    const float l_pair = sum_xor32(st.l);
     const bool empty = st.rmax == -INFINITY;
     const float m_nat = empty ? -INFINITY : st.rmax * p.scale;
     const float beta = empty ? 0.f : exp2_hw(st.m - st.rmax * p.scale_log2);
@@ -1410,7 +1477,7 @@ void kf_attn_decode_short_kernel(AttnParams p) {
     float lsum = 0.f;
 #pragma unroll
     for (int b = 0; b < NST; ++b) lsum += block_exp(s[b], p.scale_log2, neg_m, pp[2 * b], pp[2 * b + 1]);
-    const float l = lsum + __shfl_xor(lsum, 32);
+    const float l = sum_xor32(lsum);
 
     // ---- O^T = V^T P^T; V^T fragments by ds_read_b64_tr_b16 from the slot. ----
     // 16-lane group G = l / 16, w = l % 16 supplies key row 4 (G / 2) + w / 4
@@ -1442,49 +1509,52 @@ void kf_attn_decode_short_kernel(AttnParams p) {
         }
     }
 
-    // ---- Output: this split's partial, or the final row with one split. ----
+    // ---- Output: this split's partial, or the final row with one split (the
+    // choice, and the output format, made once: not per store). ----
     if (row < R) {
-        const float inv = empty ? 0.f : 1.0f / l;
+        const float m_nat = empty ? -INFINITY : mx * p.scale;
+        if (ns > 1) {
 #pragma unroll
-        for (int td = 0; td < kNTD; ++td)
+            for (int td = 0; td < kNTD; ++td)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int d = 32 * td + 8 * i + 4 * g;
-                if (d < D) {
-                    const f32x4 v = {o[td][4 * i], o[td][4 * i + 1], o[td][4 * i + 2], o[td][4 * i + 3]};
-                    if (ns == 1)
-                        store_out4(p, ri * D + d, v * inv);
-                    else
-                        *reinterpret_cast<f32x4*>(p.Opart + pi * D + d) = v;
+                for (int i = 0; i < 4; ++i) {
+                    const int d = 32 * td + 8 * i + 4 * g;
+                    if (d < D)
+                        *reinterpret_cast<f32x4*>(p.Opart + pi * D + d) =
+                            f32x4{o[td][4 * i], o[td][4 * i + 1], o[td][4 * i + 2], o[td][4 * i + 3]};
                 }
-            }
-        if (g == 0) {
-            const float m_nat = empty ? -INFINITY : mx * p.scale;
-            if (ns == 1) {
-                store_stats(p, ri, m_nat, empty ? 0.f : l);
-            } else {
+            if (g == 0) {
                 p.Mpart[pi] = m_nat;
                 p.Lpart[pi] = empty ? 0.f : l;
             }
+        } else {
+            const float inv = empty ? 0.f : 1.0f / l;
+            if (p.out_dtype == kOutF16)
+                store_o_row<kOutF16, D>(p, ri, o, inv, g);
+            else if (p.out_dtype == kOutBF16)
+                store_o_row<kOutBF16, D>(p, ri, o, inv, g);
+            else
+                store_o_row<kOutF32, D>(p, ri, o, inv, g);
+            if (g == 0) store_stats(p, ri, m_nat, empty ? 0.f : l);
         }
     }
 }
 
 // ---------------------------------------------------------------------------
 // Split merge: one wave per (query row, block of CW float4 columns of O);
-// CW is a power of two in [4, D/4] chosen by the host.  Lane l owns column
-// c = cb * CW + l % CW and the splits k = l / CW + i * (64 / CW), i < NPER
-// (NPER, a power of two <= kMergePer, covers n_splits).  Every load (partial
-// O, M, l) is unconditional and issued before the first use, so the merge
-// costs one memory round trip; the reductions over the 64 / CW lanes of a
-// column are in-wave shuffles (no LDS, no barrier).  Every wave of a row
+// CW is a power of two in [4, min(D/4, 64)] chosen by the host.  Lane l owns
+// column c = cb * CW + l % CW and the splits k = l / CW + i * (64 / CW),
+// i < NPER (NPER, a power of two <= kMergePer, covers n_splits).  Every load
+// (partial O, M, l) is unconditional and issued before the first use, so the
+// merge costs one memory round trip; the reductions over the 64 / CW lanes of
+// a column are VALU cross-lane operations (reduce_mod).  Every wave of a row
 // computes the row's max and l itself.  The planner never makes more splits
 // than kMergeMaxSplits = kMergePer * 16.
 //   O = sum_k w_k O_k / sum_k w_k l_k,  w_k = exp(M_k - max_j M_j),
 //   Mi = max_k M_k,  Li = sum_k w_k l_k.
 // ---------------------------------------------------------------------------
 constexpr int kMergeThreads = 64;
-constexpr int kMergePer = 16;                  // most splits per lane
+constexpr int kMergePer = 16;                    // most splits per lane
 constexpr int kMergeMaxSplits = kMergePer * 16;  // CW = 4: 16 split lanes
 
 // Float4 columns per merge wave for ns splits: the widest block whose
@@ -1496,6 +1566,8 @@ constexpr int merge_cols(int D, int ns) {
 }
 
 // Splits per lane (a power of two) for ns splits over 64 / cw split lanes.
+// A block narrower than min(D/4, 64) is only chosen when it needs all
+// kMergePer.
 constexpr int merge_per_lane(int cw, int ns) {
     const int need = (ns + 64 / cw - 1) / (64 / cw);
     int per = 1;
@@ -1503,27 +1575,28 @@ constexpr int merge_per_lane(int cw, int ns) {
     return per;
 }
 
-template <int D, int NPER>
+template <int D, int NPER, int CW>
 __global__ __launch_bounds__(kMergeThreads)
-void kf_attn_split_merge_kernel(AttnParams p, int cw) {
+void kf_attn_split_merge_kernel(AttnParams p) {
     static_assert(NPER >= 1 && NPER <= kMergePer, "splits per lane");
+    static_assert(CW >= 4 && CW <= 64 && CW <= D / 4 && (CW & (CW - 1)) == 0, "column block");
+    constexpr int kNCB = (D / 4) / CW;             // column blocks per row
+    constexpr int kSL = 64 / CW;                   // split lanes per column
     const int lane = threadIdx.x;
-    const int ncb = (D / 4) / cw;                  // column blocks per row
-    const int row = blockIdx.x / ncb;              // global query row
-    const int cb = blockIdx.x % ncb;
+    const int row = blockIdx.x / kNCB;             // global query row
+    const int cb = blockIdx.x % kNCB;
     const int R = p.rows_per_group;
     const int grp = row / R, r = row % R;
-    const int ns = p.n_splits;                     // 1 .. NPER * 64 / cw
-    const int sl_n = 64 / cw;                      // split lanes per column
+    const int ns = p.n_splits;                     // 1 .. NPER * kSL
     const size_t base = (size_t)grp * ns * R + r;  // partial index of split 0
-    const int c = cb * cw + (lane & (cw - 1)), sl = lane / cw;
+    const int c = cb * CW + lane % CW, sl = lane / CW;
 
     f32x4 o[NPER];
     float mk[NPER], lk[NPER];
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
         // Splits past ns read split ns - 1 and get weight 0 below.
-        const size_t pi = base + (size_t)min(sl + i * sl_n, ns - 1) * R;
+        const size_t pi = base + (size_t)min(sl + i * kSL, ns - 1) * R;
         o[i] = *reinterpret_cast<const f32x4*>(p.Opart + pi * D + 4 * c);
         mk[i] = p.Mpart[pi];
         lk[i] = p.Lpart[pi];
@@ -1531,25 +1604,23 @@ void kf_attn_split_merge_kernel(AttnParams p, int cw) {
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NPER; ++i)
-        if (sl + i * sl_n < ns) m = fmaxf(m, mk[i]);
-    for (int off = cw; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if (sl + i * kSL < ns) m = fmaxf(m, mk[i]);
+    m = reduce_mod<CW, true>(m);
     const bool none = m == -INFINITY;  // no split saw a key for this row
     float l = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
-        const bool live = sl + i * sl_n < ns && !none;
+        const bool live = sl + i * kSL < ns && !none;
         const float w = live ? exp2_hw((mk[i] - m) * kLog2e) : 0.f;
         l += w * lk[i];
         acc += w * o[i];
     }
-    for (int off = cw; off < 64; off <<= 1) {
-        l += __shfl_xor(l, off);
-        acc.x += __shfl_xor(acc.x, off);
-        acc.y += __shfl_xor(acc.y, off);
-        acc.z += __shfl_xor(acc.z, off);
-        acc.w += __shfl_xor(acc.w, off);
-    }
+    l = reduce_mod<CW, false>(l);
+    acc.x = reduce_mod<CW, false>(acc.x);
+    acc.y = reduce_mod<CW, false>(acc.y);
+    acc.z = reduce_mod<CW, false>(acc.z);
+    acc.w = reduce_mod<CW, false>(acc.w);
     if (sl == 0) {
         store_out4(p, (size_t)row * D + 4 * c, acc * (l > 0.f ? 1.0f / l : 0.f));
         if (c == 0) store_stats(p, row, m, l);
