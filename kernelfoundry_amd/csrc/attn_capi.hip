@@ -206,44 +206,58 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || pl.path != KF_PATH_DECODE_SPLIT) return e;
     const dim3 mgrid(pl.rows_total * ((D / 4) / pl.merge_cw)), mblock(kf::kMergeThreads);
+    // The (column block, splits per lane) pairs merge_cols / merge_per_lane
+    // produce: the widest block with up to kMergeTarget (kMergePer when the
+    // widest is 4) splits per lane, narrower blocks with kMergeTarget, and
+    // CW = 4 with kMergePer.
     constexpr int kCWMax = D / 4 < 64 ? D / 4 : 64;
-    if (pl.merge_cw == kCWMax) {
-        switch (pl.merge_per) {
+    constexpr int kT = kf::kMergeTarget, kP = kf::kMergePer;
+    const int cw = pl.merge_cw, per = pl.merge_per;
+    if (cw == kCWMax) {
+        switch (per) {
             case 1: kf::kf_attn_split_merge_kernel<D, 1, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
             case 2: kf::kf_attn_split_merge_kernel<D, 2, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
             case 4: kf::kf_attn_split_merge_kernel<D, 4, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
-            case 8: kf::kf_attn_split_merge_kernel<D, 8, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
-            case 16: kf::kf_attn_split_merge_kernel<D, 16, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
-            default: return hipErrorInvalidValue;  // the planner caps n_splits at kMergeMaxSplits
+            case kT: kf::kf_attn_split_merge_kernel<D, kT, kCWMax><<<mgrid, mblock, 0, stream>>>(prm); break;
+            case kP:
+                if constexpr (kCWMax == 4) {  // D = 16: the widest block is the narrowest
+                    kf::kf_attn_split_merge_kernel<D, kP, 4><<<mgrid, mblock, 0, stream>>>(prm);
+                    break;
+                } else {
+                    return hipErrorInvalidValue;  // not planned
+                }
+            default: return hipErrorInvalidValue;
         }
-    } else {
-        // Narrower column blocks are only planned with kMergePer splits per lane.
-        if (pl.merge_per != kf::kMergePer) return hipErrorInvalidValue;
-        switch (pl.merge_cw) {
-            case 4: kf::kf_attn_split_merge_kernel<D, kf::kMergePer, 4><<<mgrid, mblock, 0, stream>>>(prm); break;
+    } else if (cw == 4 && per == kP) {
+        kf::kf_attn_split_merge_kernel<D, kP, 4><<<mgrid, mblock, 0, stream>>>(prm);
+    } else if (per == kT) {
+        switch (cw) {
+            case 4: kf::kf_attn_split_merge_kernel<D, kT, 4><<<mgrid, mblock, 0, stream>>>(prm); break;
             case 8:
                 if constexpr (kCWMax > 8) {
-                    kf::kf_attn_split_merge_kernel<D, kf::kMergePer, 8><<<mgrid, mblock, 0, stream>>>(prm);
+                    kf::kf_attn_split_merge_kernel<D, kT, 8><<<mgrid, mblock, 0, stream>>>(prm);
                     break;
                 } else {
                     return hipErrorInvalidValue;
                 }
             case 16:
                 if constexpr (kCWMax > 16) {
-                    kf::kf_attn_split_merge_kernel<D, kf::kMergePer, 16><<<mgrid, mblock, 0, stream>>>(prm);
+                    kf::kf_attn_split_merge_kernel<D, kT, 16><<<mgrid, mblock, 0, stream>>>(prm);
                     break;
                 } else {
                     return hipErrorInvalidValue;
                 }
             case 32:
                 if constexpr (kCWMax > 32) {
-                    kf::kf_attn_split_merge_kernel<D, kf::kMergePer, 32><<<mgrid, mblock, 0, stream>>>(prm);
+                    kf::kf_attn_split_merge_kernel<D, kT, 32><<<mgrid, mblock, 0, stream>>>(prm);
                     break;
                 } else {
                     return hipErrorInvalidValue;
                 }
             default: return hipErrorInvalidValue;
         }
+    } else {
+        return hipErrorInvalidValue;  // not a pair the planner makes
     }
     return hipGetLastError();
 }

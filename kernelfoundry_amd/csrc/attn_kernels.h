@@ -1548,26 +1548,30 @@ void kf_attn_decode_short_kernel(AttnParams p) {
 // (partial O, M, l) is unconditional and issued before the first use, so the
 // merge costs one memory round trip; the reductions over the 64 / CW lanes of
 // a column are VALU cross-lane operations (reduce_mod).  Every wave of a row
-// computes the row's max and l itself.  The planner never makes more splits
-// than kMergeMaxSplits = kMergePer * 16.
+// computes the row's max and l itself.  Waves are dealt to the XCDs like the
+// decode workgroups (xcd_remap over a grid ordered by group), so a group's
+// partials are read on the XCD whose L2 received them.  The planner never
+// makes more splits than kMergeMaxSplits = kMergePer * 16.
 //   O = sum_k w_k O_k / sum_k w_k l_k,  w_k = exp(M_k - max_j M_j),
 //   Mi = max_k M_k,  Li = sum_k w_k l_k.
 // ---------------------------------------------------------------------------
 constexpr int kMergeThreads = 64;
 constexpr int kMergePer = 16;                    // most splits per lane
+constexpr int kMergeTarget = 8;                  // splits per lane the planner aims for
 constexpr int kMergeMaxSplits = kMergePer * 16;  // CW = 4: 16 split lanes
 
 // Float4 columns per merge wave for ns splits: the widest block whose
-// 64 / CW split lanes cover ns with at most kMergePer splits each.
+// 64 / CW split lanes cover ns with at most kMergeTarget splits each (at
+// CW = 4, up to kMergePer).
 constexpr int merge_cols(int D, int ns) {
     int cw = D / 4 < 64 ? D / 4 : 64;
-    while (cw > 4 && (ns + 64 / cw - 1) / (64 / cw) > kMergePer) cw /= 2;
+    while (cw > 4 && (ns + 64 / cw - 1) / (64 / cw) > kMergeTarget) cw /= 2;
     return cw;
 }
 
 // Splits per lane (a power of two) for ns splits over 64 / cw split lanes.
-// A block narrower than min(D/4, 64) is only chosen when it needs all
-// kMergePer.
+// A block narrower than min(D/4, 64) is only chosen with kMergeTarget
+// splits per lane, or kMergePer at CW = 4.
 constexpr int merge_per_lane(int cw, int ns) {
     const int need = (ns + 64 / cw - 1) / (64 / cw);
     int per = 1;
@@ -1583,8 +1587,9 @@ void kf_attn_split_merge_kernel(AttnParams p) {
     constexpr int kNCB = (D / 4) / CW;             // column blocks per row
     constexpr int kSL = 64 / CW;                   // split lanes per column
     const int lane = threadIdx.x;
-    const int row = blockIdx.x / kNCB;             // global query row
-    const int cb = blockIdx.x % kNCB;
+    const int mb = xcd_remap(blockIdx.x, gridDim.x);
+    const int row = mb / kNCB;                     // global query row
+    const int cb = mb % kNCB;
     const int R = p.rows_per_group;
     const int grp = row / R, r = row % R;
     const int ns = p.n_splits;                     // 1 .. NPER * kSL
