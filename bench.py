@@ -33,6 +33,11 @@ launch on the launch stream.  ``cpu_baseline`` times the repo's NumPy
 restatement of the reference's CPU path (kernel_models/flash_attn.py:250-265)
 on a bounded sample of the same workload on this host's cores.
 
+Timing protocol per workload: ``SETTLE_S`` seconds of untimed launches (the
+clocks reach their loaded steady state), W untimed warmup steps, then K timed
+back-to-back steps between two events on the launch stream, with a
+synchronize on both sides.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
 from __future__ import annotations
@@ -120,9 +125,26 @@ class Runner:
         return j
 
 
+SETTLE_S = 0.1  # untimed launches per workload before its warmup steps
+
+
+def settle(torch, runner, seconds=SETTLE_S):
+    """Untimed launches for about `seconds` of wall time.  The GPU's clocks
+    ramp up under sustained load: measured on MI355X, the first 100 prefill
+    steps after 10 warmup launches (27 ms) ran at 288 us per step, every later
+    pass at 268 us.  This runs before the W warmup steps so that the K timed
+    steps see the steady-state clock."""
+    t = time.perf_counter()
+    while time.perf_counter() - t < seconds:
+        for _ in range(16):
+            runner.launch()
+        torch.cuda.synchronize()
+
+
 def time_steps(torch, runner, steps, warmup):
     """Whole-step wall time over `steps` back-to-back launches, plus the
     average per-launch duration from an event pair around every launch."""
+    settle(torch, runner)
     for _ in range(warmup):
         runner.launch()
     torch.cuda.synchronize()
@@ -419,6 +441,7 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
+        "clock_settle_s": SETTLE_S,
         "ms_per_step": round(pre["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
