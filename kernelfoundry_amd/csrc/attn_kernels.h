@@ -453,6 +453,7 @@ struct RowState {
     float m;     // running max used for exponentiation, log2 units
     float rmax;  // true running max of the raw (unscaled) scores
     float l;     // this lane's partial sum of exp2(s*scale_log2 - m)
+    float thr;   // raw score above which m must move: (m + kLazyRescaleLog2) / scale_log2
 };
 
 // Online-softmax update for NSB score blocks: moves the running max (lazily),
@@ -644,10 +645,11 @@ __device__ __forceinline__ void block_mask(f32x16 (&s)[NSB], int lim, int lane) 
             if (32 * b + acc_row(r, lane) >= lim) s[b][r] = -INFINITY;
 }
 
-// exp2 + fp16 pack of one 32-row score block; returns its contribution to the
-// row sum (the fp16 P values, summed with v_dot2_f32_f16).
-__device__ __forceinline__ float block_exp(const f32x16& s, float scale_log2, float neg_m,
-                                           f16x8& p0, f16x8& p1) {
+// exp2 + fp16 pack of one 32-row score block; adds its fp16 P values to the
+// row sum `acc` (v_dot2_f32_f16, two terms per instruction, chained straight
+// into the running sum: no partial sums to initialise and add).
+__device__ __forceinline__ void block_exp(const f32x16& s, float scale_log2, float neg_m,
+                                          f16x8& p0, f16x8& p1, float& acc) {
     f32x8 e0, e1;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -657,34 +659,37 @@ __device__ __forceinline__ float block_exp(const f32x16& s, float scale_log2, fl
     p0 = __builtin_convertvector(e0, f16x8);
     p1 = __builtin_convertvector(e1, f16x8);
     const f16x2 ones = {(f16)1.0f, (f16)1.0f};
-    float a = 0.f, b = 0.f;
+    float a = acc;
     a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p0, p0, 0, 1), ones, a, false);
-    b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 0, 1), ones, b, false);
     a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p0, p0, 2, 3), ones, a, false);
-    b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 2, 3), ones, b, false);
     a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p0, p0, 4, 5), ones, a, false);
-    b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 4, 5), ones, b, false);
     a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p0, p0, 6, 7), ones, a, false);
-    b = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 6, 7), ones, b, false);
-    return a + b;
+    a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 0, 1), ones, a, false);
+    a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 2, 3), ones, a, false);
+    a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 4, 5), ones, a, false);
+    a = __builtin_amdgcn_fdot2(__builtin_shufflevector(p1, p1, 6, 7), ones, a, false);
+    acc = a;
 }
 
 // Move the running max for a new block max (lazily) and rescale O and l.
+// The test against the raw threshold st.thr is one compare per tile; the
+// scaled max and the new threshold are computed only when some lane moves.
 template <int NTD>
 __device__ __forceinline__ void block_update_max(RowState& st, float mx, float scale_log2,
-                                                 f32x16 (&o)[NTD]) {
+                                                 float inv_scale_log2, f32x16 (&o)[NTD]) {
     st.rmax = fmaxf(st.rmax, mx);
-    const float mt = mx * scale_log2;
-    const bool need = mt > st.m + kLazyRescaleLog2;
+    const bool need = mx > st.thr;
     if (__any(need)) {
         // Lanes that keep their max scale by exactly 1 (also when it is still
         // -inf, a fully masked row: exp2(-inf - -inf) would be NaN).
+        const float mt = mx * scale_log2;
         const float mnew = need ? mt : st.m;
         const float alpha = need ? exp2_hw(st.m - mt) : 1.0f;
         st.l *= alpha;
 #pragma unroll
         for (int td = 0; td < NTD; ++td) o[td] *= alpha;
         st.m = mnew;
+        st.thr = (mnew + kLazyRescaleLog2) * inv_scale_log2;
     }
 }
 
@@ -912,11 +917,11 @@ void kf_attn_prefill_kernel(AttnParams p) {
                 o[td] = mfma32(a, pp[jj], o[td]);
             }
     };
-    auto softmax_exp = [&](const f32x16 (&s)[kNSB], float neg_m, f16x8 (&pp)[2 * kNSB]) {
-        float sum = 0.f;
+    // Adds the tile's fp16 P values to the row sum `acc`.
+    auto softmax_exp = [&](const f32x16 (&s)[kNSB], float neg_m, f16x8 (&pp)[2 * kNSB],
+                           float& acc) {
 #pragma unroll
-        for (int b = 0; b < kNSB; ++b) sum += block_exp(s[b], c, neg_m, pp[2 * b], pp[2 * b + 1]);
-        return sum;
+        for (int b = 0; b < kNSB; ++b) block_exp(s[b], c, neg_m, pp[2 * b], pp[2 * b + 1], acc);
     };
 
     const int row = rt * kPrefillRows + wave * 32 + (lane & 31);
@@ -951,14 +956,15 @@ void kf_attn_prefill_kernel(AttnParams p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
-    RowState st{-INFINITY, -INFINITY, 0.f};
+    RowState st{-INFINITY, -INFINITY, 0.f, -INFINITY};
+    const float inv_c = 1.0f / c;
     f32x16 o[kNTD];
 #pragma unroll
     for (int td = 0; td < kNTD; ++td) o[td] = f32x16{};
     f32x16 sc[kNSB];
     qk(b0, qf, sc);
     if (BC > wave_min) block_mask<kNSB>(sc, lim_lane, lane);
-    block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, o);
+    block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, inv_c, o);
     // Exponent offset; a row with no key yet (masked) keeps m = -inf and
     // must get P = 0, not NaN.
     auto neg_m = [&]() { return ((kMask || KS > 1) && st.m == -INFINITY) ? 0.f : -st.m; };
@@ -980,9 +986,9 @@ void kf_attn_prefill_kernel(AttnParams p) {
             if (t > 0) {
                 qk(cur, qf, sc);
                 if ((t + 1) * BC > wave_min) block_mask<kNSB>(sc, lim_lane - t * BC, lane);
-                block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, o);
+                block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, inv_c, o);
             }
-            st.l += softmax_exp(sc, neg_m(), pp);
+            softmax_exp(sc, neg_m(), pp, st.l);
             pv(cur, pp, o);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();  // stage t+1 landed; every wave is done with stage t
@@ -999,7 +1005,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
         }
         f32x16 sn[kNSB];
         qk(nxt, qf, sn);
-        st.l += softmax_exp(sc, neg_m(), pp);
+        softmax_exp(sc, neg_m(), pp, st.l);
         pv(cur, pp, o);
         float mx = block_rowmax<kNSB>(sn);
         if (t + 1 < ntiles) {
@@ -1010,7 +1016,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
                 block_mask<kNSB>(sn, lim_lane - (t + 1) * BC, lane);
                 mx = block_rowmax<kNSB>(sn);
             }
-            block_update_max<kNTD>(st, mx, c, o);
+            block_update_max<kNTD>(st, mx, c, inv_c, o);
 #pragma unroll
             for (int b = 0; b < kNSB; ++b) sc[b] = sn[b];
         }
@@ -1233,7 +1239,7 @@ void kf_attn_decode_kernel(AttnParams p) {
         for (int i = lane; i < (32 - D) * G::kVtStride; i += 64) Vt[D * G::kVtStride + i] = (f16)0.f;
     }
 
-    RowState st{-INFINITY, -INFINITY, 0.f};
+    RowState st{-INFINITY, -INFINITY, 0.f, -INFINITY};
     f32x16 o[G::kNTD];
 #pragma unroll
     for (int td = 0; td < G::kNTD; ++td) o[td] = f32x16{};
@@ -1476,7 +1482,7 @@ void kf_attn_decode_short_kernel(AttnParams p) {
     f16x8 pp[2 * NST];
     float lsum = 0.f;
 #pragma unroll
-    for (int b = 0; b < NST; ++b) lsum += block_exp(s[b], p.scale_log2, neg_m, pp[2 * b], pp[2 * b + 1]);
+    for (int b = 0; b < NST; ++b) block_exp(s[b], p.scale_log2, neg_m, pp[2 * b], pp[2 * b + 1], lsum);
     const float l = sum_xor32(lsum);
 
     // ---- O^T = V^T P^T; V^T fragments by ds_read_b64_tr_b16 from the slot. ----
