@@ -51,7 +51,7 @@ enum kf_status {
     KF_ERR_WORKSPACE = 5,  /* workspace missing or smaller than required        */
     KF_ERR_ALIGN = 6,      /* a device pointer is not 16-byte aligned           */
     KF_ERR_HIP = 7,        /* a HIP runtime call failed: kf_last_hip_error()    */
-    KF_ERR_FLAGS = 8       /* kf_attn_fwd_ex: unknown bits in `flags`            */
+    KF_ERR_FLAGS = 8       /* unknown bits in `flags`, or F16 and BF16 together  */
 };
 
 /* kf_attn_fwd_ex / kf_attn_decode_paged flags. */

@@ -452,7 +452,7 @@ const char* kf_status_string(int status) {
         case KF_ERR_WORKSPACE: return "workspace missing or smaller than kf_attn_workspace_bytes()";
         case KF_ERR_ALIGN: return "device pointer not 16-byte aligned (workspace: 256-byte)";
         case KF_ERR_HIP: return "HIP runtime error (see kf_last_hip_error)";
-        case KF_ERR_FLAGS: return "unknown flag bits (only KF_ATTN_CAUSAL is defined)";
+        case KF_ERR_FLAGS: return "unknown or conflicting flag bits (KF_ATTN_CAUSAL, KF_ATTN_OUT_F16 or KF_ATTN_OUT_BF16, KF_ATTN_LSE)";
         default: return "unknown status";
     }
 }

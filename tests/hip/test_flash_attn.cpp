@@ -148,9 +148,17 @@ static bool run_case(int B, int q_len, int kv_len, int H_q, int H_kv, int D, uin
 // The extensions through kf/flash_attn.hpp, checked for exact agreement with
 // the paths above: kf::attn_fwd_ex without masking and with every key count
 // equal to kv_len, paged decode over pages holding the cache rows in order,
-// and an fp16 O equal to the round-to-nearest-even of the fp32 O.
+// and an fp16 O equal to the round-to-nearest-even of the fp32 O.  Paged
+// decode always runs the streaming decode kernel; the batch is large enough
+// for the contiguous plan to run it too (same splits, same arithmetic), which
+// the plan check below confirms.
 static bool run_extension_checks() {
-    const int B = 2, H_q = 32, H_kv = 8, D = 128, q_len = 1, kv_len = 1024, page = 16;
+    const int B = 12, H_q = 32, H_kv = 8, D = 128, q_len = 1, kv_len = 4096, page = 16;
+    kf_attn_plan_t plan;
+    if (kf_attn_plan(B, q_len, kv_len, H_q, H_kv, D, &plan) != KF_OK || plan.splits_per_block != 1) {
+        std::printf("  FAIL: the contiguous plan no longer uses the streaming decode kernel\n");
+        return false;
+    }
     const int pages = kv_len / page;
     const size_t qn = (size_t)B * H_q * q_len * D, kvn = (size_t)B * H_kv * kv_len * D;
     std::mt19937 rng(777);
@@ -224,6 +232,71 @@ static bool run_extension_checks() {
     return ok;
 }
 
+// The asynchronous launcher on two streams at once: each stream gets its own
+// cached split-KV workspace, so decodes of different inputs queued on two
+// streams (which the GPU may run concurrently) each equal the result of the
+// same decode run alone.  Every launch writes its own output buffer and all
+// of them are compared bitwise.
+static bool run_two_stream_check() {
+    const int B = 1, H_q = 32, H_kv = 8, D = 128, q_len = 1, kv_len = 4096, iters = 16;
+    const size_t qn = (size_t)B * H_q * q_len * D, kvn = (size_t)B * H_kv * kv_len * D;
+    std::mt19937 rng(4242);
+    std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
+    uint16_t *dq[2], *dk[2], *dv[2];
+    for (int i = 0; i < 2; ++i) {
+        std::vector<uint16_t> q16(qn), k16(kvn), v16(kvn);
+        for (auto& x : q16) x = kf_oracle_float_to_half(dist(rng));
+        for (auto& x : k16) x = kf_oracle_float_to_half(dist(rng));
+        for (auto& x : v16) x = kf_oracle_float_to_half(dist(rng));
+        HIP_CHECK(hipMalloc(&dq[i], qn * 2));
+        HIP_CHECK(hipMalloc(&dk[i], kvn * 2));
+        HIP_CHECK(hipMalloc(&dv[i], kvn * 2));
+        HIP_CHECK(hipMemcpy(dq[i], q16.data(), qn * 2, hipMemcpyHostToDevice));
+        HIP_CHECK(hipMemcpy(dk[i], k16.data(), kvn * 2, hipMemcpyHostToDevice));
+        HIP_CHECK(hipMemcpy(dv[i], v16.data(), kvn * 2, hipMemcpyHostToDevice));
+    }
+    float* dref[2];
+    float* dout[2][iters];
+    for (int i = 0; i < 2; ++i) {
+        HIP_CHECK(hipMalloc(&dref[i], qn * 4));
+        for (int it = 0; it < iters; ++it) HIP_CHECK(hipMalloc(&dout[i][it], qn * 4));
+    }
+    // References: one input set at a time on the null stream.
+    for (int i = 0; i < 2; ++i) {
+        HIP_CHECK(launch_flash_attn(dq[i], dk[i], dv[i], dref[i], B, q_len, kv_len, H_q, H_kv, D,
+                                    nullptr));
+        HIP_CHECK(hipDeviceSynchronize());
+    }
+    hipStream_t st[2];
+    for (int i = 0; i < 2; ++i) HIP_CHECK(hipStreamCreate(&st[i]));
+    for (int it = 0; it < iters; ++it)
+        for (int i = 0; i < 2; ++i)
+            HIP_CHECK(launch_flash_attn(dq[i], dk[i], dv[i], dout[i][it], B, q_len, kv_len, H_q,
+                                        H_kv, D, st[i]));
+    HIP_CHECK(hipDeviceSynchronize());
+    size_t bad = 0;
+    std::vector<float> ref(qn), got(qn);
+    for (int i = 0; i < 2; ++i) {
+        HIP_CHECK(hipMemcpy(ref.data(), dref[i], qn * 4, hipMemcpyDeviceToHost));
+        for (int it = 0; it < iters; ++it) {
+            HIP_CHECK(hipMemcpy(got.data(), dout[i][it], qn * 4, hipMemcpyDeviceToHost));
+            for (size_t e = 0; e < qn; ++e) bad += got[e] != ref[e];
+        }
+    }
+    for (int i = 0; i < 2; ++i) {
+        HIP_CHECK(hipStreamDestroy(st[i]));
+        (void)hipFree(dq[i]);
+        (void)hipFree(dk[i]);
+        (void)hipFree(dv[i]);
+        (void)hipFree(dref[i]);
+        for (int it = 0; it < iters; ++it) (void)hipFree(dout[i][it]);
+    }
+    const bool ok = bad == 0;
+    std::printf("  two streams x %d split-KV decodes (kv_len=%d) ... %s (differing elements: %zu)\n",
+                iters, kv_len, ok ? "PASS" : "FAIL", bad);
+    return ok;
+}
+
 int main() {
     std::printf("=== kernelfoundry_amd flash-attention end-to-end tests (gfx950) ===\n");
     int failed = 0;
@@ -255,6 +328,8 @@ int main() {
 
     std::printf("[extensions through kf/flash_attn.hpp: exact agreement]\n");
     if (!run_extension_checks()) ++failed;
+    std::printf("[asynchronous launcher on two streams: per-stream workspace]\n");
+    if (!run_two_stream_check()) ++failed;
 
     if (failed) {
         std::printf("%d test(s) FAILED\n", failed);
