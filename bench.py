@@ -23,8 +23,9 @@ half of the metric):
                      pool twice the needed size (the reference's worst-case
                      fragmentation, bench_flash_attn2.py:153-215); bytes =
                      configs[4]'s plus the block table.
-  * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep)
-                     and the MQA D=64 configs[3].
+  * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep),
+                     the MQA D=64 configs[3] and the configs[2] shape at
+                     D=256 (the reference's largest head dimension).
 
 FLOPs = 4*B*H_q*q_len*kv_len*D and bytes = fp16 Q + unique fp16 K,V + fp32 O
 (tests/bench_flash_attn.cu:125-131).  ``roofline.achieved`` divides those by
@@ -422,6 +423,7 @@ def main():
     print("bench: sweep", file=sys.stderr, flush=True)
     sweep = [run_prefill(S) for S in (512, 1024, 2048)]
     sweep.append(run_prefill(2048, H_kv=1, D=64))
+    sweep.append(run_prefill(4096, H_kv=8, D=256))
     dq, _ = run_decode(1, 2048, 1, D=64, H_kv=1)
     sweep.append({"mqa_decode_d64": dq})
     torch.cuda.empty_cache()

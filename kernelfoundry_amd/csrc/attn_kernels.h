@@ -23,8 +23,9 @@
 // Behaviour follows the reference forward (kernels/flash_attn.cu:384-585):
 // O = softmax(Q K^T / sqrt(D)) V per (b, h_q) with h_kv = h_q / (H_q / H_kv)
 // (:406), fp16 inputs, fp32 accumulation and softmax, P rounded to fp16
-// before the P.V product (:301-303) while the row sum uses the fp32 P
-// (:284-294), O divided by the row sum once at the end (:582-584), and the
+// before the P.V product (:301-303; the row sum here adds those same fp16
+// values, where the reference adds the fp32 P, :284-294: at most 2^-12
+// relative apart), O divided by the row sum once at the end (:582-584), and the
 // row statistics Mi = max_j s_ij and Li = sum_j exp(s_ij - Mi) written once
 // (:559-579).  The tiling, data layout, MFMA formulation and split-KV path
 // are this library's own (see the comments at each kernel).
@@ -563,11 +564,10 @@ template <> struct SwizzleRow<128> {
 };
 template <> struct SwizzleRow<256> : SwizzleRow<128> {};
 
-// Per head dimension: waves per workgroup (32 query rows each) and whether
-// S(t+1) = K Q^T is overlapped with the softmax of tile t (that needs a second
-// score block in registers).  D = 256 holds 128 fp32 O accumulators per lane,
-// so it runs at most 4 waves (one per SIMD, up to 512 registers) without the
-// overlap.  Grids too small to give every CU a workgroup use fewer rows per
+// Per head dimension: waves per workgroup (32 query rows each).  Every
+// variant overlaps S(t+1) = K Q^T with the softmax of tile t (a second score
+// block in registers).  D = 256 holds 128 fp32 O accumulators per lane, so it
+// runs 4 waves (one per SIMD, up to 512 registers; it uses ~450).  Grids too small to give every CU a workgroup use fewer rows per
 // workgroup: KS = 2 KV groups (each wave takes half of the keys of its rows,
 // the two halves merged in LDS at the end) and then fewer waves (NW = 4, 2).
 template <int D> constexpr int kPrefillMaxWaves = D >= 256 ? 4 : 8;
@@ -586,16 +586,13 @@ template <int D, int NW = kPrefillMaxWaves<D>, int KS = 1> struct PrefillCfg {
     // whatever the workgroup size, so every variant keeps its accumulators in
     // VGPRs; 512 for D = 256.
     static constexpr int kWavesPerEU = D >= 256 ? 1 : 2;
-    // Pipelined: stages t, t+1 and the one being filled rotate through three
-    // LDS buffers; otherwise two suffice (and keep every LDS offset of D = 256
-    // inside the 16-bit instruction offset field).
-    static constexpr bool kPipeline = D <= 128;
-    // Tiles per LDS stage.  Pipelined 8-wave workgroups without KV groups
-    // hold two tiles per stage, so the workgroup barrier and the LDS-DMA issue
-    // come once per 64 kv rows.  The others keep one tile per stage (48 KB of
-    // LDS per KV group at D = 128), which holds the compiler to the
-    // 256-register budget.
-    static constexpr int kSub = (kPipeline && kWaves >= 8 && KS == 1) ? 2 : 1;
+    // Stages t, t+1 and the one being filled rotate through three LDS
+    // buffers.  Tiles per LDS stage: 8-wave workgroups without KV groups hold
+    // two tiles per stage, so the workgroup barrier and the LDS-DMA issue come
+    // once per 64 kv rows.  The others keep one tile per stage (48 KB of LDS
+    // per KV group at D = 128, 96 KB in all at D = 256), which holds the
+    // compiler to the 256-register budget at D <= 128.
+    static constexpr int kSub = (kWaves >= 8 && KS == 1) ? 2 : 1;
     static constexpr int kStageRows = BC * kSub;
 };
 
@@ -717,10 +714,9 @@ void kf_attn_prefill_kernel(AttnParams p) {
     using SW = SwizzleRow<D>;
     constexpr int kNKK = D / 16;                  // MFMA k-steps over D
     constexpr int kNTD = (D < 32 ? 32 : D) / 32;  // 32-row O^T tiles
-    constexpr bool kPipe = Cfg::kPipeline;
     __shared__ __attribute__((aligned(1024))) char buf0[KS * S::kStageBytes];
     __shared__ __attribute__((aligned(1024))) char buf1[KS * S::kStageBytes];
-    __shared__ __attribute__((aligned(1024))) char buf2[kPipe ? KS * S::kStageBytes : 16];
+    __shared__ __attribute__((aligned(1024))) char buf2[KS * S::kStageBytes];
     __shared__ __attribute__((aligned(16))) char zero_pad[16];  // D=16: V^T rows 16..31
 
     const int tid = threadIdx.x;
@@ -782,7 +778,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     if constexpr (KS > 1) wave_min = min(wave_min, kv_end) - kv_base;
     char* const b0 = buf0 + kgrp * S::kStageBytes;  // this group's stage regions
     char* const b1 = buf1 + kgrp * S::kStageBytes;
-    char* const b2 = buf2 + (kPipe ? kgrp * S::kStageBytes : 0);
+    char* const b2 = buf2 + kgrp * S::kStageBytes;
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
     const char* Kh = reinterpret_cast<const char*>(p.K + (size_t)grp * kv_len * D);
@@ -947,7 +943,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
 
     // ---- Prologue: stage 0 (and 1 when pipelined) in flight, Q fragments, S(0). ----
     issue_stage(b0, 0);
-    if (kPipe && nstages > 1) issue_stage(b1, SR);
+    if (nstages > 1) issue_stage(b1, SR);
     f16x8 qf[kNKK];
     load_q_frags<D>(Qg, row, R, lane, qf);
     if constexpr (D < 32) {
@@ -980,20 +976,6 @@ void kf_attn_prefill_kernel(AttnParams p) {
     // overlap MFMA and VALU work that is interleaved in its own stream).
     auto tile = [&](const char* cur, const char* nxt, char* fill, int t, bool sync) {
         f16x8 pp[2 * kNSB];
-        if constexpr (!kPipe) {
-            // Two buffers: stage t+1 loads into `nxt` while stage t is used.
-            if (t + 1 < ntiles) issue_stage(const_cast<char*>(nxt), (t + 1) * BC);
-            if (t > 0) {
-                qk(cur, qf, sc);
-                if ((t + 1) * BC > wave_min) block_mask<kNSB>(sc, lim_lane - t * BC, lane);
-                block_update_max<kNTD>(st, block_rowmax<kNSB>(sc), c, inv_c, o);
-            }
-            softmax_exp(sc, neg_m(), pp, st.l);
-            pv(cur, pp, o);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();  // stage t+1 landed; every wave is done with stage t
-            return;
-        }
         if (sync) {
             // Tile t is the last of its stage j = t / kSub, tile t+1 the first
             // of stage j+1: wait until stage j+1 landed for every wave; stage
@@ -1021,7 +1003,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
             for (int b = 0; b < kNSB; ++b) sc[b] = sn[b];
         }
     };
-    if constexpr (kPipe && kSub == 1) {
+    if constexpr (kSub == 1) {
         for (int t = 0; t < ntiles; t += 3) {
             tile(b0, b1, b2, t, true);
             if (t + 1 >= ntiles) break;
@@ -1029,8 +1011,8 @@ void kf_attn_prefill_kernel(AttnParams p) {
             if (t + 2 >= ntiles) break;
             tile(b2, b0, b1, t + 2, true);
         }
-    } else if constexpr (kPipe) {
-        static_assert(kSub == 2, "pipelined stages hold one or two tiles");
+    } else {
+        static_assert(kSub == 2, "stages hold one or two tiles");
         // Tile t reads the (t % 2)-th half of stage t / 2, which lives in
         // buffer (t / 2) % 3; the loop body covers 3 stages.
         constexpr int H = BC * S::kRowBytes;
@@ -1046,12 +1028,6 @@ void kf_attn_prefill_kernel(AttnParams p) {
             tile(b2, b2 + H, nullptr, t + 4, false);
             if (t + 5 >= ntiles) break;
             tile(b2 + H, b0, b1, t + 5, true);
-        }
-    } else {
-        for (int t = 0; t < ntiles; t += 2) {
-            tile(b0, b1, nullptr, t, false);
-            if (t + 1 >= ntiles) break;
-            tile(b1, b0, nullptr, t + 1, false);
         }
     }
 

@@ -63,7 +63,7 @@ MASKED_CASES = [
     (1, 8, 2, 256, 256, 128, True, None),              # causal square, GQA
     (2, 4, 1, 100, 300, 64, True, None),               # causal, q_len < kv_len, ragged
     (1, 4, 4, 64, 64, 16, True, None),                 # D=16
-    (1, 4, 2, 130, 130, 256, True, None),              # D=256 (two-buffer path)
+    (1, 4, 2, 130, 130, 256, True, None),              # D=256 (4-wave pipelined path)
     (1, 4, 1, 300, 200, 128, True, None),              # q_len > kv_len: top rows see nothing
     (1, 8, 8, 513, 513, 128, True, None),              # MHA, several row tiles + tail
     (3, 8, 2, 200, 256, 128, False, [256, 1, 137]),    # per-sequence keys, prefill

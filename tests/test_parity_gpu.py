@@ -27,14 +27,15 @@ def _torch():
     return torch
 
 
-def _run_kf(q16, k16, v16):
-    """Upload fp16 numpy arrays, run kf_attn_fwd, return (O, Mi, Li) numpy."""
+def _run_kf(q16, k16, v16, causal=False):
+    """Upload fp16 numpy arrays, run kf_attn_fwd (kf_attn_fwd_ex when causal),
+    return (O, Mi, Li) numpy."""
     import kernelfoundry_amd as kf
     torch = _torch()
     Q = torch.from_numpy(np.ascontiguousarray(q16)).cuda()
     K = torch.from_numpy(np.ascontiguousarray(k16)).cuda()
     V = torch.from_numpy(np.ascontiguousarray(v16)).cuda()
-    O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True)
+    O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True, causal=causal)
     torch.cuda.synchronize()
     return O.cpu().numpy(), Mi.cpu().numpy(), Li.cpu().numpy()
 
@@ -196,6 +197,24 @@ def test_config_c3_gqa_prefill(S):
     O, Mi, Li = _run_kf(q16, k16, v16)
     _property_checks(O, Mi, Li, v16, H_q, H_kv)
     _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (0, 13), (0, 31)])
+
+
+@pytest.mark.parametrize("S,causal", [(2048, False), (1536, True)])
+def test_d256_prefill_long(S, causal):
+    """D = 256 (4-wave workgroups, one per SIMD, three-stage pipelined loop)
+    over many tiles: full-size properties and sampled heads against the fp64
+    oracle, causal included."""
+    B, H_q, H_kv, D = 1, 16, 4, 256
+    _announce(test="d256_long", S=S, causal=causal)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, S, S, D, 6000 + S)
+    O, Mi, Li = _run_kf(q16, k16, v16, causal=causal)
+    _property_checks(O, Mi, Li, v16, H_q, H_kv)
+    for b, h in [(0, 0), (0, 9), (0, 15)]:
+        hk = h // (H_q // H_kv)
+        Or, Mr, Lr = orc.sdpa(q16[b:b + 1, h:h + 1], k16[b:b + 1, hk:hk + 1],
+                              v16[b:b + 1, hk:hk + 1], causal=causal)
+        _check(O[b:b + 1, h:h + 1], Or, f"D=256 S={S} causal={causal} head {h}")
+        _check_stats(Mi[b:b + 1, h:h + 1], Li[b:b + 1, h:h + 1], Mr, Lr, f"D=256 head {h}")
 
 
 def test_config_c2_gqa_decode():
