@@ -878,8 +878,10 @@ void kf_attn_prefill_kernel(AttnParams p) {
     }
 
     auto qk = [&](const char* stage, const f16x8 (&qf)[kNKK], f32x16 (&s)[kNSB]) {
-        // K fragments are fetched in batches of up to 8 (32 VGPRs).
-        constexpr int kBatch = kNKK < 8 ? kNKK : (D >= 256 ? 4 : 8);
+        // K fragments are fetched in batches: 8 (32 VGPRs) at D <= 128 under
+        // the 256-register budget; all 16 of a tile at D = 256, whose one wave
+        // per SIMD has the registers (measured 4 % faster than batches of 4).
+        constexpr int kBatch = kNKK < 8 ? kNKK : (D >= 256 ? 16 : 8);
 #pragma unroll
         for (int b = 0; b < kNSB; ++b) {
             s[b] = f32x16{};
