@@ -443,6 +443,27 @@ __device__ __forceinline__ f32x16 qk_block(const f16* __restrict__ Ks, int row0,
     return s;
 }
 
+// qk_block with the Q^T fragments read from an LDS copy of the 32 query rows
+// (row r's chunk c at chunk c ^ (r & 15), D / 8 chunks per row).
+template <int D, int BC>
+__device__ __forceinline__ f32x16 qk_block_qlds(const f16* __restrict__ Ks, const char* q_lds,
+                                                int lane) {
+    using G = StageGeom<D, BC>;
+    const int row = lane & 31;
+    const int g = lane >> 5;
+    const f16* base = Ks + row * D;
+    const char* qrow = q_lds + row * D * 2;
+    f32x16 s = {};
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+        const int phys = (2 * kk + g) ^ (row & G::kSwz);
+        const f16x8 a = *reinterpret_cast<const f16x8*>(base + phys * 8);
+        const f16x8 q = *reinterpret_cast<const f16x8*>(qrow + ((2 * kk + g) ^ (row & 15)) * 16);
+        s = mfma32(a, q, s);
+    }
+    return s;
+}
+
 // kv offset (within its 32-row block) of accumulator register r on lane l.
 __device__ __forceinline__ int acc_row(int r, int lane) {
     return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -1182,7 +1203,14 @@ __global__ __launch_bounds__(kDecodeThreads, DecodeCfg<D>::kWavesPerEU)
 void kf_attn_decode_kernel(AttnParams p) {
     using G = StageGeom<D, kDecodeStage>;
     using SM = DecodeSmem<D>;
+    // D = 256: the Q^T fragments (64 registers) are read from an LDS copy of
+    // the group's 32 query rows at every stage instead of being held, which
+    // keeps the register-staged K/V stage, the O accumulators and the rest
+    // within the register file (held in registers they spilled to scratch
+    // inside the stage loop).
+    constexpr bool kQLds = D >= 256;
     __shared__ __attribute__((aligned(16))) char smem_raw[SM::kBytes];
+    __shared__ __attribute__((aligned(16))) char q_lds[kQLds ? 32 * D * 2 : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1207,8 +1235,21 @@ void kf_attn_decode_kernel(AttnParams p) {
     const int bseq = grp / p.heads_kv, hkv = grp % p.heads_kv;  // paged addressing
 
     const int row = lane & 31;
-    f16x8 qf[D / 16];
-    load_q_frags<D>(Qg, row, R, lane, qf);
+    f16x8 qf[kQLds ? 1 : D / 16];
+    if constexpr (kQLds) {
+        // Row r (rows >= R repeat row R - 1), 16-byte chunk c stored at chunk
+        // c ^ (r & 15) of LDS row r, so that the 32 rows read by one fragment
+        // load spread over the banks.
+        constexpr int kChunks = D / 8;
+        for (int i = tid; i < 32 * kChunks; i += kDecodeThreads) {
+            const int r = i / kChunks, c = i % kChunks;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(Qg + (size_t)min(r, R - 1) * D + c * 8);
+            *reinterpret_cast<u32x4*>(q_lds + (r * kChunks + (c ^ (r & 15))) * 16) = v;
+        }
+        __syncthreads();
+    } else {
+        load_q_frags<D>(Qg, row, R, lane, qf);
+    }
     const int lim_lane = row < R ? row_kv_limit(p, kvb, row % p.q_len) : kvb;
 
     f16* Ks = reinterpret_cast<f16*>(smem_raw) + wave * G::kStageHalfs;
@@ -1242,7 +1283,10 @@ void kf_attn_decode_kernel(AttnParams p) {
         if (kv_next < s1) load_stage(kv_next, pn);
 
         f32x16 s[1];
-        s[0] = qk_block<D, kDecodeStage>(Ks, 0, qf, lane);
+        if constexpr (kQLds)
+            s[0] = qk_block_qlds<D, kDecodeStage>(Ks, q_lds, lane);
+        else
+            s[0] = qk_block<D, kDecodeStage>(Ks, 0, qf, lane);
         if (kv0 + kDecodeStage > min(s1, lim_min) || !(pc.ok_lo && pc.ok_hi)) {
             const int lim = min(s1, lim_lane) - kv0;
 #pragma unroll

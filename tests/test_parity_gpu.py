@@ -122,6 +122,28 @@ def test_parity_with_stats(case):
     _check_stats(Mi, Li, Mr, Lr, str(case))
 
 
+@pytest.mark.parametrize("B,q_len,kv_len,causal,ragged", [(12, 1, 2000, False, False),
+                                                         (12, 2, 1500, True, True)])
+def test_d256_streaming_decode(B, q_len, kv_len, causal, ragged):
+    """D = 256 on the streaming decode kernel (Q^T fragments read from LDS at
+    every stage), with its split merge; key counts and causal masking."""
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    H_q, H_kv, D = 16, 4, 256
+    pl = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
+    assert pl.path == "decode_split" and pl.splits_per_block == 1, pl
+    _announce(test="d256_streaming", B=B, q_len=q_len, kv_len=kv_len, causal=causal, ragged=ragged)
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, q_len, kv_len, D, 7000 + q_len)
+    lens = [kv_len - 97 * b for b in range(B)] if ragged else None
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    kv_t = torch.tensor(lens, dtype=torch.int32, device="cuda") if ragged else None
+    O, Mi, Li = kf.attn_fwd(t(q16), t(k16), t(v16), return_stats=True, causal=causal, kv_lens=kv_t)
+    torch.cuda.synchronize()
+    Or, Mr, Lr = orc.sdpa(q16, k16, v16, causal=causal, kv_lens=lens)
+    _check(O.cpu().numpy(), Or, "D=256 streaming decode")
+    _check_stats(Mi.cpu().numpy(), Li.cpu().numpy(), Mr, Lr, "D=256 streaming decode")
+
+
 @pytest.mark.parametrize("q_len", [1, 5, 40])
 def test_kv_len_one_returns_v0(q_len):
     """KV_len = 1: the softmax weight is 1, so O = V_0 and Li = 1.
