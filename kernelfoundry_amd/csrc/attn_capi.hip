@@ -15,8 +15,31 @@ namespace {
 
 constexpr int kNumCUs = 256;            // MI355X compute units
 constexpr int kDecodeMaxRows = 32;      // query rows per KV head on the decode path
-constexpr int kDecodeTargetBlocks = 2 * kNumCUs;
-constexpr int kDecodeMinSplitRows = 4 * kf::kDecodeStage;  // one stage per wave
+// Streaming decode: a split holds at least one 32-key stage per wave.
+inline int decode_min_split_rows(int D) { return kf::decode_waves(D) * kf::kDecodeStage; }
+
+// Splits per KV head for the streaming decode kernel, before the caps.
+// D <= 128 (8-wave workgroups, one per CU by LDS): the fewest splits whose
+// busiest CU streams at most 2 % more than an even share, where a CU streams
+// ceil(n_groups * s / CUs) workgroups of 1 / s of a head each (96 heads: 8
+// splits = 3 full rounds, not 3 splits = 1 round plus a 32-workgroup tail).
+// D = 256 (4 waves, one workgroup per CU): two workgroups per CU, which
+// measured 3 % faster than one.
+long long decode_stream_splits(long long n_groups, long long max_splits, int D) {
+    if (D >= 256) return (2LL * kNumCUs + n_groups - 1) / n_groups;
+    const double even = (double)n_groups / kNumCUs;
+    long long best = 1;
+    double best_t = 1e300;
+    for (long long s = 1; s <= max_splits; ++s) {
+        const double t = (double)((n_groups * s + kNumCUs - 1) / kNumCUs) / (double)s;
+        if (t <= even * 1.02) return s;
+        if (t < best_t * 0.98) {
+            best = s;
+            best_t = t;
+        }
+    }
+    return best;
+}
 // Short-split decode (one wave per split of 32 or 64 keys): used while the
 // job is at most kShortMaxWaves such waves (8 per CU); beyond it the work is
 // bandwidth-bound and the streaming decode kernel takes over.  64-key splits
@@ -91,8 +114,10 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl, 
             p.grid = (int)((n_groups * splits + kf::kShortWaves - 1) / kf::kShortWaves);
             p.threads = 64 * kf::kShortWaves;
         } else {
-            splits = (kDecodeTargetBlocks + n_groups - 1) / n_groups;
-            const long long max_splits = (kv_len + kDecodeMinSplitRows - 1) / kDecodeMinSplitRows;
+            long long max_splits = kv_len / decode_min_split_rows(D);
+            if (max_splits < 1) max_splits = 1;
+            if (max_splits > kf::kMergeMaxSplits) max_splits = kf::kMergeMaxSplits;
+            splits = decode_stream_splits(n_groups, max_splits, D);
             if (splits > max_splits) splits = max_splits;
             if (splits > kf::kMergeMaxSplits) splits = kf::kMergeMaxSplits;
             if (splits < 1) splits = 1;
@@ -101,7 +126,7 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl, 
             splits = (kv_len + per - 1) / per;
             if (n_groups * splits > INT_MAX) return KF_ERR_SIZE;
             p.grid = (int)(n_groups * splits);
-            p.threads = kf::kDecodeThreads;
+            p.threads = 64 * kf::decode_waves(D);
         }
         p.short_stages = nst;
         p.n_splits = (int)splits;

@@ -14,7 +14,7 @@
 //                              split-KV ("flash-decoding") for <= 32 query
 //                              rows per KV head (Q_len = 1 decode, GQA/MQA
 //                              groups): every wave streams its own KV stages
-//                              through a wave-private LDS slot; the 4 waves of
+//                              through a wave-private LDS slot; the waves of
 //                              a workgroup merge in LDS; with several splits
 //                              each workgroup writes an unnormalised partial;
 //                              kPaged reads K/V through a block table.
@@ -588,9 +588,10 @@ template <> struct SwizzleRow<256> : SwizzleRow<128> {};
 // Per head dimension: waves per workgroup (32 query rows each).  Every
 // variant overlaps S(t+1) = K Q^T with the softmax of tile t (a second score
 // block in registers).  D = 256 holds 128 fp32 O accumulators per lane, so it
-// runs 4 waves (one per SIMD, up to 512 registers; it uses ~450).  Grids too small to give every CU a workgroup use fewer rows per
-// workgroup: KS = 2 KV groups (each wave takes half of the keys of its rows,
-// the two halves merged in LDS at the end) and then fewer waves (NW = 4, 2).
+// runs 4 waves (one per SIMD, up to 512 registers; it uses ~450).  Grids too
+// small to give every CU a workgroup use fewer rows per workgroup: KS = 2 KV
+// groups (each wave takes half of the keys of its rows, the two halves merged
+// in LDS at the end) and then fewer waves (NW = 4, 2).
 template <int D> constexpr int kPrefillMaxWaves = D >= 256 ? 4 : 8;
 
 constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
@@ -1148,23 +1149,29 @@ void kf_attn_prefill_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode (split-KV): <= 32 query rows per KV head.  Workgroup = 4 waves on one
-// (group, split); wave w streams 32-row stages w, w+4, w+8, ... of the split
-// through its own LDS slot (single buffer, next stage prefetched into
+// Decode (split-KV): <= 32 query rows per KV head.  Workgroup = NW waves on
+// one (group, split); wave w streams 32-row stages w, w+NW, w+2NW, ... of the
+// split through its own LDS slot (single buffer, next stage prefetched into
 // registers while the current one is computed; no workgroup barrier in the
-// loop).  The 4 wave states merge in LDS at the end.
+// loop).  The NW wave states merge in LDS at the end.  D <= 128 runs 8 waves,
+// one workgroup per CU (its LDS), D = 256 4 waves (one per SIMD).
 // ---------------------------------------------------------------------------
-constexpr int kDecodeThreads = 256;
 constexpr int kDecodeStage = 32;
 
-template <int D> struct DecodeCfg { static constexpr int kWavesPerEU = D >= 256 ? 1 : 2; };
+template <int D> struct DecodeCfg {
+    static constexpr int kWaves = D >= 256 ? 4 : 8;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kWavesPerEU = D >= 256 ? 1 : 2;
+};
+inline int decode_waves(int D) { return D >= 256 ? DecodeCfg<256>::kWaves : DecodeCfg<128>::kWaves; }
 
 template <int D>
 struct DecodeSmem {
     using G = StageGeom<D, kDecodeStage>;
+    static constexpr int NW = DecodeCfg<D>::kWaves;
     static constexpr int kOStride = D + 4;  // floats per merged-O row (padded)
-    static constexpr int kStageBytes = 4 * G::kStageHalfs * 2;
-    static constexpr int kMergeBytes = 4 * 32 * kOStride * 4 + 4 * 32 * 2 * 4;
+    static constexpr int kStageBytes = NW * G::kStageHalfs * 2;
+    static constexpr int kMergeBytes = NW * 32 * kOStride * 4 + NW * 32 * 2 * 4;
     static constexpr int kBytes = kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes;
 };
 
@@ -1199,10 +1206,12 @@ __device__ __forceinline__ PagedStage paged_stage(const AttnParams& p, int bseq,
 
 // kPaged: K / V are page pools addressed through p.block_table.
 template <int D, bool kPaged>
-__global__ __launch_bounds__(kDecodeThreads, DecodeCfg<D>::kWavesPerEU)
+__global__ __launch_bounds__(DecodeCfg<D>::kThreads, DecodeCfg<D>::kWavesPerEU)
 void kf_attn_decode_kernel(AttnParams p) {
     using G = StageGeom<D, kDecodeStage>;
     using SM = DecodeSmem<D>;
+    constexpr int NW = DecodeCfg<D>::kWaves;
+    constexpr int kThreads = DecodeCfg<D>::kThreads;
     // D = 256: the Q^T fragments (64 registers) are read from an LDS copy of
     // the group's 32 query rows at every stage instead of being held, which
     // keeps the register-staged K/V stage, the O accumulators and the rest
@@ -1241,7 +1250,7 @@ void kf_attn_decode_kernel(AttnParams p) {
         // c ^ (r & 15) of LDS row r, so that the 32 rows read by one fragment
         // load spread over the banks.
         constexpr int kChunks = D / 8;
-        for (int i = tid; i < 32 * kChunks; i += kDecodeThreads) {
+        for (int i = tid; i < 32 * kChunks; i += kThreads) {
             const int r = i / kChunks, c = i % kChunks;
             const u32x4 v = *reinterpret_cast<const u32x4*>(Qg + (size_t)min(r, R - 1) * D + c * 8);
             *reinterpret_cast<u32x4*>(q_lds + (r * kChunks + (c ^ (r & 15))) * 16) = v;
@@ -1279,7 +1288,7 @@ void kf_attn_decode_kernel(AttnParams p) {
         wave_lds_sync();  // previous stage's LDS reads are done
         ld.store(Ks, Vt, lane);
         wave_lds_sync();
-        const int kv_next = kv0 + 4 * kDecodeStage;
+        const int kv_next = kv0 + NW * kDecodeStage;
         if (kv_next < s1) load_stage(kv_next, pn);
 
         f32x16 s[1];
@@ -1310,8 +1319,8 @@ void kf_attn_decode_kernel(AttnParams p) {
 
     __syncthreads();  // all waves are done with their stage slots
     float* Ob = reinterpret_cast<float*>(smem_raw);
-    float* Mb = Ob + 4 * 32 * SM::kOStride;
-    float* Lb = Mb + 4 * 32;
+    float* Mb = Ob + NW * 32 * SM::kOStride;
+    float* Lb = Mb + NW * 32;
 #pragma unroll
     for (int td = 0; td < G::kNTD; ++td)
 #pragma unroll
@@ -1329,20 +1338,20 @@ void kf_attn_decode_kernel(AttnParams p) {
     }
     __syncthreads();
 
-    // Merge the 4 wave states: thread -> (query row, kSeg-wide d segment).
+    // Merge the NW wave states: thread -> (query row, kSeg-wide d segment).
     constexpr int kTpr = D / 4 < 8 ? D / 4 : 8;  // threads per query row
     constexpr int kSeg = D / kTpr;                // multiple of 4
-    static_assert(kDecodeThreads / kTpr >= 32, "merge must cover 32 rows in one pass");
+    static_assert(kThreads / kTpr >= 32, "merge must cover 32 rows in one pass");
     const int mrow = tid / kTpr;
     const int seg = tid % kTpr;
     if (mrow < R) {
         float m = Mb[mrow];
 #pragma unroll
-        for (int w = 1; w < 4; ++w) m = fmaxf(m, Mb[w * 32 + mrow]);
-        float wt[4];
+        for (int w = 1; w < NW; ++w) m = fmaxf(m, Mb[w * 32 + mrow]);
+        float wt[NW];
         float l = 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float mw = Mb[w * 32 + mrow];
             wt[w] = mw == -INFINITY ? 0.f : exp2_hw((mw - m) * kLog2e);
             l += wt[w] * Lb[w * 32 + mrow];
@@ -1357,7 +1366,7 @@ void kf_attn_decode_kernel(AttnParams p) {
             const int d = seg * kSeg + j;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
+            for (int w = 0; w < NW; ++w) {
                 const f32x4 v = *reinterpret_cast<const f32x4*>(Ob + (w * 32 + mrow) * SM::kOStride + d);
                 acc += wt[w] * v;
             }

@@ -156,9 +156,10 @@ def test_plans_for_baseline_configs():
     p = kf.plan(1, 1, 2048, 32, 1, 64)               # C4b MQA decode
     assert p.path == "decode_split" and p.rows_per_group == 32
     assert p.splits_per_block == 4 and p.num_splits == 64 and p.grid_blocks == 16
-    p = kf.plan(32, 1, 8192, 32, 8, 128)             # C5 batched decode: streaming kernel
-    assert p.path == "decode_split" and p.grid_blocks == 256 * p.num_splits
-    assert p.splits_per_block == 1 and p.num_splits == 2
+    p = kf.plan(32, 1, 8192, 32, 8, 128)             # C5 batched decode: streaming kernel,
+    assert p.path == "decode" and p.grid_blocks == 256  # one 8-wave workgroup per KV head
+    assert p.splits_per_block == 1 and p.num_splits == 1 and p.block_threads == 512
+    assert p.workspace_bytes == 0                        # and no split merge
 
 
 @pytest.mark.parametrize("B,q,kv,H_q,H_kv,D", [
@@ -177,8 +178,12 @@ def test_decode_split_geometry_covers_kv(B, q, kv, H_q, H_kv, D):
         assert p.kv_per_split in ((32, 64) if D <= 128 else (32,))
         assert p.grid_blocks == -(-splits // 4) and p.block_threads == 256 and splits <= 2048
     else:
-        assert p.splits_per_block == 1 and p.grid_blocks == splits and p.block_threads == 256
-        assert p.kv_per_split >= 128 or p.num_splits == 1
+        # Streaming kernel: 8 waves (4 at D = 256), at least one 32-key stage
+        # per wave in every split.
+        waves = 8 if D <= 128 else 4
+        assert p.splits_per_block == 1 and p.grid_blocks == splits
+        assert p.block_threads == 64 * waves
+        assert p.kv_per_split >= 32 * waves or p.num_splits == 1
     if p.num_splits == 1:
         assert p.path == "decode" and p.workspace_bytes == 0
     else:
@@ -189,17 +194,21 @@ def test_decode_split_geometry_covers_kv(B, q, kv, H_q, H_kv, D):
 
 
 @pytest.mark.parametrize("B,H_kv,kv,D,splits,per_block", [
-    (1, 8, 131072, 128, 64, 1), (1, 1, 262144, 128, 256, 1), (1, 1, 65536, 64, 256, 1),
-    (1, 1, 1 << 20, 16, 256, 1), (1, 4, 40000, 256, 125, 1), (1, 8, 8192, 128, 128, 4),
-    (1, 8, 4096, 128, 128, 4), (1, 8, 16384, 128, 256, 4), (2, 8, 16384, 128, 32, 1),
+    (1, 8, 131072, 128, 32, 1), (1, 1, 262144, 128, 249, 1), (1, 1, 65536, 64, 228, 1),
+    (1, 1, 1 << 20, 16, 251, 1), (1, 4, 40000, 256, 125, 1), (1, 8, 8192, 128, 128, 4),
+    (1, 8, 4096, 128, 128, 4), (1, 8, 16384, 128, 256, 4), (2, 8, 16384, 128, 16, 1),
+    (12, 8, 4096, 128, 8, 1), (32, 8, 8192, 128, 1, 1),
 ])
 def test_decode_split_counts(B, H_kv, kv, D, splits, per_block):
-    """Streaming decode: splits target 2 workgroups per CU, at most the 256
-    partials the split merge reads in one pass.  Short-split decode: 64-key
-    splits while they give 4 waves per CU, else 32-key ones, up to 8 waves
-    per CU and 256 splits."""
+    """Streaming decode (one 8-wave workgroup per CU at D <= 128): the fewest
+    splits whose busiest CU streams within 2 % of an even share of the heads
+    (96 heads: 8 splits = 3 full rounds of 256 workgroups), at most the 256
+    partials the split merge reads in one pass, the key counts then rounded
+    to whole 32-key stages; D = 256 (4 waves) aims at two workgroups per CU.
+    Short-split decode: 64-key splits while they give 4 waves per CU, else
+    32-key ones, up to 8 waves per CU and 256 splits."""
     p = kf.plan(B, 1, kv, 32, H_kv, D)
-    assert p.path == "decode_split" and p.num_splits == splits
+    assert p.path == ("decode_split" if splits > 1 else "decode") and p.num_splits == splits
     assert p.splits_per_block == per_block
     assert p.num_splits * p.kv_per_split >= kv
 
@@ -275,10 +284,11 @@ def test_paged_decode_validation():
     assert _paged(flags=16) == kf.KF_ERR_FLAGS
     assert _paged(flags=kf.KF_ATTN_OUT_F16 | kf.KF_ATTN_OUT_BF16) == kf.KF_ERR_FLAGS
     need = kf.paged_workspace_bytes(2, 1, 32, 8, 128, 16, 64)
-    # Paged decode always runs the streaming kernel: 8 splits of 128 keys over
-    # the 1024-key capacity, each a partial of 2 x 32 rows of D + 2 floats (the
-    # same shape unpaged runs 32-key one-wave splits).
-    assert need == 8 * 64 * (128 + 2) * 4
+    # Paged decode always runs the streaming kernel: 4 splits of 256 keys (one
+    # 32-key stage per wave of an 8-wave workgroup) over the 1024-key
+    # capacity, each a partial of 2 x 32 rows of D + 2 floats (the same shape
+    # unpaged runs 32-key one-wave splits).
+    assert need == 4 * 64 * (128 + 2) * 4
     assert kf.workspace_bytes(2, 1, 64 * 16, 32, 8, 128) == 32 * 64 * (128 + 2) * 4
     assert _paged(ws_bytes=need - 1) == kf.KF_ERR_WORKSPACE
     assert kf.paged_workspace_bytes(2, 9, 32, 8, 128, 16, 64) == 0    # not a decode shape

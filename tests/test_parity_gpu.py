@@ -273,11 +273,11 @@ def test_config_c5_batched_long_decode():
     _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (7, 9), (31, 31), (16, 4)])
 
 
-@pytest.mark.parametrize("H_q,H_kv,kv,splits", [(32, 8, 131072, 64), (32, 1, 262144, 256)])
+@pytest.mark.parametrize("H_q,H_kv,kv,splits", [(32, 8, 131072, 32), (32, 1, 262144, 249)])
 def test_long_context_decode(H_q, H_kv, kv, splits):
     """One sequence of 128 K / 256 K keys (GQA and MQA with 32 query rows per
-    KV head) on the streaming decode kernel: 2 workgroups per CU, the MQA
-    case stopping at the merge kernel's one-pass capacity of 256 splits;
+    KV head) on the streaming decode kernel: one 8-wave workgroup per CU, the
+    MQA case close to the merge kernel's one-pass capacity of 256 splits;
     sampled heads against the oracle plus properties."""
     import kernelfoundry_amd as kf
     B, D = 1, 128
