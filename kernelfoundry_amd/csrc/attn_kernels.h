@@ -252,12 +252,6 @@ __device__ __forceinline__ float reduce_mod(float v) {
     return v;
 }
 
-__device__ __forceinline__ u32x4 load16(const uint16_t* p, bool pred) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (pred) v = *reinterpret_cast<const u32x4*>(p);
-    return v;
-}
-
 __device__ __forceinline__ f16x8 as_f16x8(const u32x4& v) { return __builtin_bit_cast(f16x8, v); }
 
 // Hardware workgroup id -> logical id such that each XCD receives one
@@ -349,33 +343,55 @@ struct StageLoader {
     // The same for a stage whose rows 0..15 start at element offset off_lo
     // and rows 16..31 at off_hi (consecutive rows D elements apart within a
     // half): a stage of a paged K/V cache.  Rows >= nrows and halves whose
-    // page is invalid (ok_* false) are zero-filled and never read.
+    // page is invalid (ok_* false) are zero-filled (their pool memory may
+    // hold anything, and 0 * NaN would be NaN) and never read as keys.  The
+    // half bases and flags are wave-uniform: the loads are unpredicated, an
+    // invalid half reads the pool's first page (always in bounds), and the
+    // rare stage with an invalid half or a short tail is zeroed afterwards
+    // in one wave-uniform branch (predicating every load cost a 64-bit
+    // address per load and spilled registers at D = 256).
     __device__ __forceinline__ void load_halves(const uint16_t* __restrict__ Kp,
                                                 const uint16_t* __restrict__ Vp, size_t off_lo,
                                                 size_t off_hi, bool ok_lo, bool ok_hi, int nrows,
                                                 int tid) {
         static_assert(BC == 32, "two 16-row halves");
+        const size_t blo = ok_lo ? off_lo : 0, bhi = ok_hi ? off_hi : 0;
 #pragma unroll
         for (int i = 0; i < kKIters; ++i) {
             const int idx = tid + i * NT;
-            const bool in = (kKTotal % NT == 0) || idx < kKTotal;
-            const int row = idx / G::kChunks, c = idx % G::kChunks;
-            const bool hi = row >= 16;
-            const size_t off = (hi ? off_hi : off_lo) + (size_t)(row & 15) * D + c * 8;
-            k[i] = load16(Kp + off, in && row < nrows && (hi ? ok_hi : ok_lo));
+            const int idc = ((kKTotal % NT == 0) || idx < kKTotal) ? idx : 0;
+            const int row = idc / G::kChunks, c = idc % G::kChunks;
+            const size_t off = (row >= 16 ? bhi : blo) + (size_t)(row & 15) * D + c * 8;
+            k[i] = *reinterpret_cast<const u32x4*>(Kp + off);
         }
+        // V: lane tid always reads rows 4 (idx % kVGroups) + r, of one half
+        // when NT is a multiple of kVGroups (it is: NT = 64, kVGroups = 8).
+        static_assert(NT % kVGroups == 0, "V rows of a lane in one half");
+        const uint16_t* vb = Vp + (4 * (tid % kVGroups) >= 16 ? bhi : blo);
 #pragma unroll
         for (int i = 0; i < kVIters; ++i) {
             const int idx = tid + i * NT;
-            const bool in = (kVTotal % NT == 0) || idx < kVTotal;
-            const int grp = idx % kVGroups, c = idx / kVGroups;
+            const int idc = ((kVTotal % NT == 0) || idx < kVTotal) ? idx : 0;
+            const int grp = idc % kVGroups, c = idc / kVGroups;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = 4 * grp + r;
-                const bool hi = row >= 16;
-                const size_t off = (hi ? off_hi : off_lo) + (size_t)(row & 15) * D + c * 8;
-                v[i][r] = load16(Vp + off, in && row < nrows && (hi ? ok_hi : ok_lo));
+                v[i][r] = *reinterpret_cast<const u32x4*>(vb + (size_t)(row & 15) * D + c * 8);
             }
+        }
+        if (!(ok_lo && ok_hi) || nrows < BC) {
+#pragma unroll
+            for (int i = 0; i < kKIters; ++i) {
+                const int row = ((tid + i * NT) % kKTotal) / G::kChunks;
+                if (!(row < nrows && (row >= 16 ? ok_hi : ok_lo))) k[i] = u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int i = 0; i < kVIters; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 4 * ((tid + i * NT) % kVGroups) + r;
+                    if (!(row < nrows && (row >= 16 ? ok_hi : ok_lo))) v[i][r] = u32x4{0u, 0u, 0u, 0u};
+                }
         }
     }
 
