@@ -1228,12 +1228,13 @@ void kf_attn_decode_kernel(AttnParams p) {
     using SM = DecodeSmem<D>;
     constexpr int NW = DecodeCfg<D>::kWaves;
     constexpr int kThreads = DecodeCfg<D>::kThreads;
-    // D = 256: the Q^T fragments (64 registers) are read from an LDS copy of
-    // the group's 32 query rows at every stage instead of being held, which
-    // keeps the register-staged K/V stage, the O accumulators and the rest
-    // within the register file (held in registers they spilled to scratch
-    // inside the stage loop).
-    constexpr bool kQLds = D >= 256;
+    // D = 256, and paged D = 128: the Q^T fragments (64 / 32 registers) are
+    // read from an LDS copy of the group's 32 query rows at every stage
+    // instead of being held, which keeps the register-staged K/V stage, the O
+    // accumulators and the paged addressing within the register file (held
+    // in registers they spilled to scratch: inside the stage loop at
+    // D = 256, around it for paged D = 128).
+    constexpr bool kQLds = D >= 256 || (kPaged && D >= 128);
     __shared__ __attribute__((aligned(16))) char smem_raw[SM::kBytes];
     __shared__ __attribute__((aligned(16))) char q_lds[kQLds ? 32 * D * 2 : 16];
 

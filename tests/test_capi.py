@@ -46,6 +46,34 @@ def test_library_carries_gfx950_code():
         assert kern in blob
 
 
+def test_no_kernel_uses_scratch(tmp_path):
+    """Every kernel of the gfx950 code object keeps its state in registers and
+    LDS: no private (scratch) segment, no spilled VGPRs.  Read from the
+    library's own code object metadata (llvm-objcopy + clang-offload-bundler
+    + llvm-readelf from the ROCm toolchain)."""
+    tools = "/opt/rocm/llvm/bin"
+    objcopy, bundler, readelf = (os.path.join(tools, t) for t in
+                                 ("llvm-objcopy", "clang-offload-bundler", "llvm-readelf"))
+    if not all(os.path.exists(t) for t in (objcopy, bundler, readelf)):
+        pytest.skip("ROCm LLVM tools not found")
+    fat, co = tmp_path / "fatbin", tmp_path / "gfx950.co"
+    subprocess.run([objcopy, "--dump-section", f".hip_fatbin={fat}", kf.LIB_PATH], check=True)
+    subprocess.run([bundler, "--unbundle", "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+                    f"--input={fat}", f"--output={co}"], check=True)
+    notes = subprocess.run([readelf, "--notes", str(co)], capture_output=True, text=True,
+                           check=True).stdout
+    kernels = {}
+    for block in re.split(r"\n\s+- \.agpr_count:", notes)[1:]:
+        name = re.search(r"\.name:\s+(\S+)", block).group(1)
+        scratch = int(re.search(r"\.private_segment_fixed_size:\s+(\d+)", block).group(1))
+        spills = int(re.search(r"\.vgpr_spill_count:\s+(\d+)", block).group(1))
+        kernels[name] = (scratch, spills)
+    assert any("kf_attn_prefill_kernel" in n for n in kernels)
+    assert any("kf_attn_decode_kernel" in n for n in kernels)
+    bad = {n: v for n, v in kernels.items() if v != (0, 0)}
+    assert not bad, f"kernels with scratch / spills: {bad}"
+
+
 def test_version(lib):
     assert b"gfx950" in lib.kf_version()
 
