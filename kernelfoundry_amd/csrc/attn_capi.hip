@@ -23,8 +23,8 @@ inline int decode_min_split_rows(int D) { return kf::decode_waves(D) * kf::kDeco
 // busiest CU streams at most 2 % more than an even share, where a CU streams
 // ceil(n_groups * s / CUs) workgroups of 1 / s of a head each (96 heads: 8
 // splits = 3 full rounds, not 3 splits = 1 round plus a 32-workgroup tail).
-// D = 256 (4 waves, one workgroup per CU): two workgroups per CU, which
-// measured 3 % faster than one.
+// D = 256 (4 waves; its LDS holds one workgroup per CU): grids of two
+// workgroups per CU, i.e. two rounds, which measured 3 % faster than one.
 long long decode_stream_splits(long long n_groups, long long max_splits, int D) {
     if (D >= 256) return (2LL * kNumCUs + n_groups - 1) / n_groups;
     const double even = (double)n_groups / kNumCUs;
