@@ -219,6 +219,34 @@ def _out_flags(torch, out_dtype, return_lse):
     return f[out_dtype] | (KF_ATTN_LSE if return_lse else 0)
 
 
+def _output(torch, out, shape, out_dtype, device):
+    """The output tensor: a new one, or the caller's after checking that the
+    kernel's writes (shape x element size of ``out_dtype``) land inside it."""
+    dtype = out_dtype or torch.float32
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    if out.dtype != dtype or tuple(out.shape) != tuple(shape) or out.device != device \
+            or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous {dtype} tensor of shape {tuple(shape)} "
+                         f"on {device}")
+    return out
+
+
+def _workspace(torch, workspace, need, device, stream):
+    """The split-KV workspace: the caller's if it is a large enough buffer on
+    the device, else a new one (kept alive until ``stream`` passes it)."""
+    if not need:
+        return None
+    if workspace is not None:
+        if workspace.device != device or not workspace.is_contiguous():
+            raise ValueError(f"workspace must be a contiguous tensor on {device}")
+        if workspace.numel() * workspace.element_size() >= need:
+            return workspace
+    workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    workspace.record_stream(stream)
+    return workspace
+
+
 def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=None,
              causal=False, kv_lens=None, out_dtype=None, return_lse=False):
     """Attention forward on torch tensors resident on the GPU.
@@ -243,12 +271,13 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
         raise ValueError("Q, K, V must be contiguous [B, H, S, D]")
     if Q.dim() != 4 or K.dim() != 4 or K.shape != V.shape:
         raise ValueError("expected Q [B,H_q,q_len,D] and K, V [B,H_kv,kv_len,D]")
+    if K.device != Q.device or V.device != Q.device:
+        raise ValueError("Q, K, V must be on one device")
     B, H_q, q_len, D = Q.shape
     Bk, H_kv, kv_len, Dk = K.shape
     if Bk != B or Dk != D:
         raise ValueError("Q and K/V disagree on B or D")
-    if out is None:
-        out = torch.empty((B, H_q, q_len, D), dtype=out_dtype or torch.float32, device=Q.device)
+    out = _output(torch, out, (B, H_q, q_len, D), out_dtype, Q.device)
     Mi = Li = None
     if return_stats or return_lse:
         Mi = torch.empty((B, H_q, q_len), dtype=torch.float32, device=Q.device)
@@ -257,12 +286,10 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
     need = workspace_bytes(B, q_len, kv_len, H_q, H_kv, D)
     if stream is None:
         stream = torch.cuda.current_stream(Q.device)
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=Q.device)
-        workspace.record_stream(stream)
+    workspace = _workspace(torch, workspace, need, Q.device, stream)
     if kv_lens is not None:
-        if kv_lens.dtype != torch.int32 or not kv_lens.is_cuda or kv_lens.numel() != B:
-            raise ValueError("kv_lens must be an int32 GPU tensor of B elements")
+        if kv_lens.dtype != torch.int32 or kv_lens.device != Q.device or kv_lens.numel() != B:
+            raise ValueError("kv_lens must be an int32 tensor of B elements on Q's device")
         kv_lens = kv_lens.contiguous()
     st = attn_fwd_ex_ptr(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(),
                          Mi.data_ptr() if Mi is not None else 0,
@@ -270,7 +297,7 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
                          B, q_len, kv_len, H_q, H_kv, D,
                          kv_lens.data_ptr() if kv_lens is not None else 0,
                          (KF_ATTN_CAUSAL if causal else 0) | flags,
-                         workspace.data_ptr() if (need and workspace is not None) else 0,
+                         workspace.data_ptr() if workspace is not None else 0,
                          need, stream.cuda_stream)
     if st != KF_OK:
         msg = status_string(st)
@@ -302,6 +329,10 @@ def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, re
     for t, name in ((block_table, "block_table"), (kv_lens, "kv_lens")):
         if t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous int32 GPU tensor")
+    if any(t.device != Q.device for t in (K_pages, V_pages, block_table, kv_lens)):
+        raise ValueError("all tensors must be on Q's device")
+    if Q.dim() != 4 or K_pages.dim() != 4:
+        raise ValueError("expected Q [B,H_q,q_len,D] and K/V pages [num_pages,H_kv,page_size,D]")
     B, H_q, q_len, D = Q.shape
     num_pages, H_kv, page_size, Dk = K_pages.shape
     if K_pages.shape != V_pages.shape or Dk != D:
@@ -309,8 +340,7 @@ def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, re
     if block_table.dim() != 2 or block_table.shape[0] != B or kv_lens.numel() != B:
         raise ValueError("block_table must be [B, max_pages_per_seq] and kv_lens [B]")
     max_pages = block_table.shape[1]
-    if out is None:
-        out = torch.empty((B, H_q, q_len, D), dtype=out_dtype or torch.float32, device=Q.device)
+    out = _output(torch, out, (B, H_q, q_len, D), out_dtype, Q.device)
     Mi = Li = None
     if return_stats or return_lse:
         Mi = torch.empty((B, H_q, q_len), dtype=torch.float32, device=Q.device)
@@ -319,16 +349,14 @@ def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, re
     need = paged_workspace_bytes(B, q_len, H_q, H_kv, D, page_size, max_pages)
     if stream is None:
         stream = torch.cuda.current_stream(Q.device)
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=Q.device)
-        workspace.record_stream(stream)
+    workspace = _workspace(torch, workspace, need, Q.device, stream)
     st = attn_decode_paged_ptr(Q.data_ptr(), K_pages.data_ptr(), V_pages.data_ptr(),
                                block_table.data_ptr(), kv_lens.data_ptr(), out.data_ptr(),
                                Mi.data_ptr() if Mi is not None else 0,
                                Li.data_ptr() if Li is not None else 0,
                                B, q_len, H_q, H_kv, D, page_size, max_pages, num_pages,
                                (KF_ATTN_CAUSAL if causal else 0) | flags,
-                               workspace.data_ptr() if (need and workspace is not None) else 0,
+                               workspace.data_ptr() if workspace is not None else 0,
                                need, stream.cuda_stream)
     if st != KF_OK:
         msg = status_string(st)

@@ -102,3 +102,43 @@ def test_paged_output_formats():
                                   _bf16_rne(O32))
     np.testing.assert_allclose(lse.cpu().numpy(), Mi.cpu().numpy() + np.log(Li.cpu().numpy()),
                                rtol=0, atol=1e-5)
+
+
+def test_python_entries_reject_buffers_the_kernels_would_overrun():
+    """A caller's O must match the shape and element size the kernels write
+    (O defaults to fp32), and a caller's workspace must be a device buffer:
+    anything else raises before any launch."""
+    import pytest
+    import torch
+
+    import kernelfoundry_amd as kf
+
+    dev = torch.device("cuda")
+    Q = torch.zeros((1, 4, 8, 64), dtype=torch.float16, device=dev)
+    K = torch.zeros((1, 2, 16, 64), dtype=torch.float16, device=dev)
+    V = torch.zeros_like(K)
+    for bad in (torch.empty((1, 4, 8, 64), dtype=torch.float16, device=dev),   # fp16, fp32 written
+                torch.empty((1, 4, 8, 32), dtype=torch.float32, device=dev),   # too few columns
+                torch.empty((1, 8, 4, 64), dtype=torch.float32, device=dev).transpose(1, 2)):
+        with pytest.raises(ValueError):
+            kf.attn_fwd(Q, K, V, out=bad)
+    with pytest.raises(ValueError):
+        kf.attn_fwd(Q, K, V, out=torch.empty((1, 4, 8, 64), dtype=torch.float32, device=dev),
+                    out_dtype=torch.bfloat16)
+    Q1 = torch.zeros((1, 4, 1, 64), dtype=torch.float16, device=dev)
+    K1 = torch.zeros((1, 2, 4096, 64), dtype=torch.float16, device=dev)
+    assert kf.plan(1, 1, 4096, 4, 2, 64).workspace_bytes > 0
+    with pytest.raises(ValueError):
+        kf.attn_fwd(Q1, K1, K1, workspace=torch.empty(1 << 24, dtype=torch.uint8))
+    # Paged decode: same rule for O.
+    Kp = torch.zeros((8, 2, 16, 64), dtype=torch.float16, device=dev)
+    table = torch.arange(8, dtype=torch.int32, device=dev).reshape(1, 8)
+    lens = torch.full((1,), 100, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        kf.attn_decode_paged(Q1, Kp, Kp, table, lens,
+                             out=torch.empty((1, 4, 1, 64), dtype=torch.float16, device=dev))
+    # The well-formed calls still run.
+    O = kf.attn_fwd(Q, K, V, out=torch.empty((1, 4, 8, 64), dtype=torch.float32, device=dev))
+    O16 = kf.attn_decode_paged(Q1, Kp, Kp, table, lens, out_dtype=torch.float16)
+    torch.cuda.synchronize()
+    assert torch.isfinite(O).all() and O16.dtype == torch.float16
