@@ -287,6 +287,12 @@ def cpu_baseline(seconds_target=12.0):
     except AttributeError:
         cores = os.cpu_count()
     threads = os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS")
+    blas = "unknown"
+    try:
+        info = np.show_config(mode="dicts")["Build Dependencies"]["blas"]
+        blas = f"{info.get('name', '?')} {info.get('version', '')}".strip()
+    except Exception:  # older numpy: no dict form
+        pass
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -304,7 +310,7 @@ def cpu_baseline(seconds_target=12.0):
                    f"(oracle.sdpa_fp32_reference_style = kernel_models/flash_attn.py:250-265), "
                    f"median of {len(runs)} runs = {sec:.2f} s ({sum(runs):.1f} s sampled); "
                    f"cpu '{cpu_model}', "
-                   f"affinity {cores} cores, BLAS threads {threads or 'default'}"),
+                   f"affinity {cores} cores, BLAS {blas}, BLAS threads {threads or 'default'}"),
     }
 
 
