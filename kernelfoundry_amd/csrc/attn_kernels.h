@@ -1,6 +1,6 @@
 // attn_kernels.h -- gfx950 (CDNA4) flash-attention forward kernels.
 //
-// Three kernels, all hand-written for wave64 and the fp16 MFMA
+// Four kernels, all hand-written for wave64 and the fp16 MFMA
 // v_mfma_f32_32x32x16_f16:
 //
 //   kf_attn_prefill_kernel<D, kMask, NW>
@@ -18,7 +18,12 @@
 //                              a workgroup merge in LDS; with several splits
 //                              each workgroup writes an unnormalised partial;
 //                              kPaged reads K/V through a block table.
-//   kf_attn_split_merge_kernel<D>  merges the split partials into O, Mi, Li.
+//   kf_attn_decode_short_kernel<D, NST>
+//                              split-KV for small decode jobs: every wave is
+//                              one split of 32 or 64 keys and issues all of
+//                              its loads at once (one memory round trip).
+//   kf_attn_split_merge_kernel<D, NPER, CW>
+//                              merges the split partials into O, Mi, Li.
 //
 // Behaviour follows the reference forward (kernels/flash_attn.cu:384-585):
 // O = softmax(Q K^T / sqrt(D)) V per (b, h_q) with h_kv = h_q / (H_q / H_kv)
