@@ -1,0 +1,56 @@
+"""Property test of the dispatch planner (kf_attn_plan, host code only) over
+random shapes: every plan covers all keys of a head exactly once with whole
+32-key stages, stays within the split merge's one-pass capacity, gives the
+streaming decode kernel at least one stage per wave in each split, and sizes
+the split workspace for every partial."""
+import pytest
+from hypothesis import given, settings, strategies as st
+
+import kernelfoundry_amd as kf
+
+RATIOS = [1, 2, 4, 8, 16, 32]
+
+
+@settings(max_examples=400, deadline=None)
+@given(B=st.integers(1, 64), H_kv=st.sampled_from([1, 2, 4, 8]), ratio=st.sampled_from(RATIOS),
+       q=st.integers(1, 300), kv=st.integers(1, 300000), D=st.sampled_from([16, 64, 128, 256]))
+def test_plan_invariants(B, H_kv, ratio, q, kv, D):
+    H_q = H_kv * ratio
+    try:
+        p = kf.plan(B, q, kv, H_q, H_kv, D)
+    except kf.KfError as e:
+        # Only shapes beyond 32-bit in-head indexing are refused.
+        assert e.status == kf.KF_ERR_SIZE
+        assert (ratio * q) * D > 2 ** 31 - 1 or kv * D > 2 ** 31 - 1 or B * H_q * q > 2 ** 31 - 1
+        return
+    R = ratio * q
+    n_groups = B * H_kv
+    assert p.rows_per_group == R
+    if p.path == "prefill":
+        assert R > 32
+        waves = p.block_threads // 64
+        assert waves in ((4,) if D == 256 else (2, 4, 8))
+        # A workgroup holds 32 query rows per wave, or 16 when its waves form
+        # two KV groups (each taking half of the keys); row tiles cover R.
+        assert p.grid_blocks % n_groups == 0
+        tiles = p.grid_blocks // n_groups
+        assert tiles in (-(-R // (32 * waves)), -(-R // (16 * waves)))
+        assert p.workspace_bytes == 0 and p.num_splits == 1
+        return
+    assert R <= 32
+    assert p.kv_per_split % 32 == 0
+    assert (p.num_splits - 1) * p.kv_per_split < kv <= p.num_splits * p.kv_per_split
+    assert p.num_splits <= 256
+    if p.splits_per_block == 4:                       # short-split kernel
+        assert p.kv_per_split in (32, 64)
+        assert p.grid_blocks * 4 >= n_groups * p.num_splits > (p.grid_blocks - 1) * 4
+    else:                                             # streaming kernel
+        waves = 8 if D <= 128 else 4
+        assert p.block_threads == 64 * waves
+        assert p.grid_blocks == n_groups * p.num_splits
+        assert p.num_splits == 1 or p.kv_per_split >= 32 * waves
+    if p.num_splits == 1:
+        assert p.path == "decode" and p.workspace_bytes == 0
+    else:
+        assert p.path == "decode_split"
+        assert p.workspace_bytes >= n_groups * p.num_splits * R * (D + 2) * 4
