@@ -430,7 +430,9 @@ def main():
     sweep = [run_prefill(S) for S in (512, 1024, 2048)]
     sweep.append(run_prefill(2048, H_kv=1, D=64))
     sweep.append(run_prefill(4096, H_kv=8, D=256))
-    dq, _ = run_decode(1, 2048, 1, D=64, H_kv=1)
+    # configs[3] decode: 0.54 MB per set, rotated over > 512 MB of distinct
+    # sets like configs[1], so each step reads HBM, not the Infinity Cache.
+    dq, _ = run_decode(1, 2048, 960, D=64, H_kv=1)
     sweep.append({"mqa_decode_d64": dq})
     torch.cuda.empty_cache()
 
