@@ -1,0 +1,41 @@
+"""GPU check at the largest key count the ABI accepts (kv_len * D just under
+2^31 elements per head: 4.3 GB each of K and V at D = 128), where element
+offsets fill 31 bits and byte offsets reach 2^32.  Closed form, no oracle
+run: every key is zero except the last one, whose score exceeds all others
+by ~90 (e^-90 underflows the fp16 P to 0), so every output row must equal
+the last V row exactly, while every other V row holds -1; Mi must be that
+score and Li exactly 1.  A wrapped or truncated offset would read another
+row and show up as -1 / a wrong Mi."""
+import math
+
+import pytest
+import torch
+
+import kernelfoundry_amd as kf
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("q_len,H_q,D", [(1, 8, 128), (64, 1, 128), (1, 8, 256)])
+def test_last_key_at_the_offset_limit(q_len, H_q, D):
+    kv = (2 ** 31 - 1) // D // 64 * 64 - 64
+    print("case", dict(q_len=q_len, H_q=H_q, D=D, kv=kv, path=kf.plan(1, q_len, kv, H_q, 1, D).path),
+          flush=True)
+    dev = torch.device("cuda")
+    K = torch.zeros((1, 1, kv, D), dtype=torch.float16, device=dev)
+    V = torch.full((1, 1, kv, D), -1.0, dtype=torch.float16, device=dev)
+    K[0, 0, -1] = 16.0
+    vlast = (torch.arange(D, device=dev, dtype=torch.float32) / D).half()
+    V[0, 0, -1] = vlast
+    Q = torch.full((1, H_q, q_len, D), 0.5, dtype=torch.float16, device=dev)
+    try:
+        O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True)
+        torch.cuda.synchronize()
+        want = vlast.float().expand(1, H_q, q_len, D)
+        assert torch.equal(O, want), (O - want).abs().max().item()
+        score = 0.5 * 16.0 * D / math.sqrt(D)      # q.k / sqrt(D)
+        assert torch.allclose(Mi, torch.full_like(Mi, score), rtol=1e-6, atol=1e-4)
+        assert torch.equal(Li, torch.ones_like(Li))
+    finally:
+        del K, V
+        torch.cuda.empty_cache()
