@@ -39,3 +39,29 @@ def test_last_key_at_the_offset_limit(q_len, H_q, D):
     finally:
         del K, V
         torch.cuda.empty_cache()
+
+
+def test_last_row_at_the_offset_limit():
+    """The same at the largest accepted query-row count (q_len * D just under
+    2^31: 4.3 GB of Q, 8.6 GB of fp32 O): every row must equal the last V
+    row, checked on the first, middle and last rows written."""
+    D, kv = 128, 64
+    q = (2 ** 31 - 1) // D // 256 * 256 - 256
+    print("case", dict(q_len=q, D=D, kv=kv, path=kf.plan(1, q, kv, 1, 1, D).path), flush=True)
+    dev = torch.device("cuda")
+    K = torch.zeros((1, 1, kv, D), dtype=torch.float16, device=dev)
+    V = torch.full((1, 1, kv, D), -1.0, dtype=torch.float16, device=dev)
+    K[0, 0, -1] = 16.0
+    vlast = (torch.arange(D, device=dev, dtype=torch.float32) / D).half()
+    V[0, 0, -1] = vlast
+    Q = torch.full((1, 1, q, D), 0.5, dtype=torch.float16, device=dev)
+    try:
+        O = kf.attn_fwd(Q, K, V)
+        torch.cuda.synchronize()
+        for rows in (slice(0, 1024), slice(q // 2, q // 2 + 1024), slice(q - 1024, q)):
+            got = O[0, 0, rows]
+            assert torch.equal(got, vlast.float().expand_as(got)), rows
+        assert torch.equal(O[0, 0, :, 0], torch.zeros(q, device=dev))  # column 0 of vlast
+    finally:
+        del Q
+        torch.cuda.empty_cache()
