@@ -65,3 +65,30 @@ def test_last_row_at_the_offset_limit():
     finally:
         del Q
         torch.cuda.empty_cache()
+
+
+def test_paged_pool_with_the_largest_page_offsets():
+    """Paged decode over a 4.3 GB page pool (2^20 pages of 16 rows, D = 128)
+    with the block table in reverse page order: the dominant key sits on the
+    highest page id, whose base offset is the largest, and must be the one
+    that every output row equals."""
+    D, ps = 128, 16
+    pages = (2 ** 31 - 1) // D // ps - 8          # key capacity within 31 bits
+    dev = torch.device("cuda")
+    Kp = torch.zeros((pages, 1, ps, D), dtype=torch.float16, device=dev)
+    Vp = torch.full((pages, 1, ps, D), -1.0, dtype=torch.float16, device=dev)
+    top, row = pages - 1, 5                        # highest page id, a row inside it
+    Kp[top, 0, row] = 16.0
+    vhit = (torch.arange(D, device=dev, dtype=torch.float32) / D).half()
+    Vp[top, 0, row] = vhit
+    table = torch.arange(pages - 1, -1, -1, dtype=torch.int32, device=dev).reshape(1, pages)
+    lens = torch.full((1,), pages * ps, dtype=torch.int32, device=dev)
+    Q = torch.full((1, 8, 1, D), 0.5, dtype=torch.float16, device=dev)
+    print("case", dict(pages=pages, keys=pages * ps), flush=True)
+    try:
+        O = kf.attn_decode_paged(Q, Kp, Vp, table, lens)
+        torch.cuda.synchronize()
+        assert torch.equal(O, vhit.float().expand_as(O)), (O - vhit.float()).abs().max().item()
+    finally:
+        del Kp, Vp
+        torch.cuda.empty_cache()
