@@ -332,7 +332,8 @@ def main():
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE {world}); the attention forward shards by KV head with no "
-              "communication, see DESIGN.md", file=sys.stderr)
+              "communication, so every GPU would run the same kernels on its share",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
