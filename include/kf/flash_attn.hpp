@@ -46,6 +46,9 @@ inline hipError_t status_to_hip(int st) {
 // one.  A buffer is grown (freed and reallocated) only after its stream has
 // drained.  Up to kMaxEntries (device, stream) pairs are kept per thread;
 // beyond that the oldest is released after a synchronisation of its device.
+// Entries are keyed by the stream handle: a stream destroyed while its
+// launches still run may hand its handle to a new stream, which would then
+// share the buffer, so synchronise a stream before destroying it.
 struct WorkspaceCache {
     struct Entry {
         int device;

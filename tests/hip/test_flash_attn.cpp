@@ -297,6 +297,59 @@ static bool run_two_stream_check() {
     return ok;
 }
 
+// More streams than the per-thread workspace cache keeps (kMaxEntries):
+// every pass over the streams evicts entries (device drain, free) and
+// allocates new ones, and every output must still equal the reference.
+static bool run_many_streams_check() {
+    const int B = 1, H_q = 32, H_kv = 8, D = 128, q_len = 1, kv_len = 4096;
+    const int n_streams = kf::WorkspaceCache::kMaxEntries + 4, passes = 2;
+    const size_t qn = (size_t)B * H_q * q_len * D, kvn = (size_t)B * H_kv * kv_len * D;
+    std::mt19937 rng(777);
+    std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
+    std::vector<uint16_t> q16(qn), k16(kvn), v16(kvn);
+    for (auto& x : q16) x = kf_oracle_float_to_half(dist(rng));
+    for (auto& x : k16) x = kf_oracle_float_to_half(dist(rng));
+    for (auto& x : v16) x = kf_oracle_float_to_half(dist(rng));
+    uint16_t *dq, *dk, *dv;
+    HIP_CHECK(hipMalloc(&dq, qn * 2));
+    HIP_CHECK(hipMalloc(&dk, kvn * 2));
+    HIP_CHECK(hipMalloc(&dv, kvn * 2));
+    HIP_CHECK(hipMemcpy(dq, q16.data(), qn * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dk, k16.data(), kvn * 2, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dv, v16.data(), kvn * 2, hipMemcpyHostToDevice));
+    float* dref;
+    HIP_CHECK(hipMalloc(&dref, qn * 4));
+    HIP_CHECK(launch_flash_attn(dq, dk, dv, dref, B, q_len, kv_len, H_q, H_kv, D, nullptr));
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<hipStream_t> st(n_streams);
+    std::vector<float*> dout((size_t)n_streams * passes);
+    for (auto& s : st) HIP_CHECK(hipStreamCreate(&s));
+    for (auto& o : dout) HIP_CHECK(hipMalloc(&o, qn * 4));
+    int max_entries = 0;
+    for (int ps = 0; ps < passes; ++ps)
+        for (int i = 0; i < n_streams; ++i) {
+            HIP_CHECK(launch_flash_attn(dq, dk, dv, dout[(size_t)ps * n_streams + i], B, q_len,
+                                        kv_len, H_q, H_kv, D, st[i]));
+            max_entries = std::max(max_entries, kf::thread_workspace().count);
+        }
+    HIP_CHECK(hipDeviceSynchronize());
+    size_t bad = 0;
+    std::vector<float> ref(qn), got(qn);
+    HIP_CHECK(hipMemcpy(ref.data(), dref, qn * 4, hipMemcpyDeviceToHost));
+    for (float* o : dout) {
+        HIP_CHECK(hipMemcpy(got.data(), o, qn * 4, hipMemcpyDeviceToHost));
+        for (size_t e = 0; e < qn; ++e) bad += got[e] != ref[e];
+    }
+    for (auto& s : st) HIP_CHECK(hipStreamDestroy(s));
+    for (float* o : dout) (void)hipFree(o);
+    for (void* ptr : {(void*)dq, (void*)dk, (void*)dv, (void*)dref}) (void)hipFree(ptr);
+    const bool ok = bad == 0 && max_entries == kf::WorkspaceCache::kMaxEntries;
+    std::printf("  %d streams x %d passes through the workspace cache (at most %d entries kept) ... "
+                "%s (differing elements: %zu)\n",
+                n_streams, passes, max_entries, ok ? "PASS" : "FAIL", bad);
+    return ok;
+}
+
 int main() {
     std::printf("=== kernelfoundry_amd flash-attention end-to-end tests (gfx950) ===\n");
     int failed = 0;
@@ -330,6 +383,7 @@ int main() {
     if (!run_extension_checks()) ++failed;
     std::printf("[asynchronous launcher on two streams: per-stream workspace]\n");
     if (!run_two_stream_check()) ++failed;
+    if (!run_many_streams_check()) ++failed;
 
     if (failed) {
         std::printf("%d test(s) FAILED\n", failed);

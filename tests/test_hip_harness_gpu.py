@@ -6,7 +6,7 @@ include/kf/flash_attn.hpp (the drop-in the integration notes describe): the
 reference's 18 prefill cases through the synchronous launch_flash_attn,
 decode and mixed-length cases through the asynchronous overload, the
 kf::attn_fwd_ex / kf::attn_decode_paged extensions, and the asynchronous
-launcher on two streams.  __graft_entry__.build() compiles it to
+launcher on two streams and on more streams than its workspace cache keeps.  __graft_entry__.build() compiles it to
 tests/hip/bin/test_flash_attn.
 """
 import os
@@ -31,6 +31,7 @@ def test_cpp_harness_passes():
     assert sum("PASS" in l for l in lines) >= 30, r.stdout
     assert not any("FAIL" in l for l in lines), r.stdout
     assert "two streams" in r.stdout
+    assert "through the workspace cache" in r.stdout
 
 
 BENCH = os.path.join(HERE, "hip", "bin", "bench_flash_attn")
