@@ -288,9 +288,12 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
         stream = torch.cuda.current_stream(Q.device)
     workspace = _workspace(torch, workspace, need, Q.device, stream)
     if kv_lens is not None:
-        if kv_lens.dtype != torch.int32 or kv_lens.device != Q.device or kv_lens.numel() != B:
-            raise ValueError("kv_lens must be an int32 tensor of B elements on Q's device")
-        kv_lens = kv_lens.contiguous()
+        # A contiguous copy would be made on torch's current stream, unordered
+        # with a launch on another ``stream``: require the caller's layout.
+        if kv_lens.dtype != torch.int32 or kv_lens.device != Q.device or kv_lens.numel() != B \
+                or not kv_lens.is_contiguous():
+            raise ValueError("kv_lens must be a contiguous int32 tensor of B elements on "
+                             "Q's device")
     st = attn_fwd_ex_ptr(Q.data_ptr(), K.data_ptr(), V.data_ptr(), out.data_ptr(),
                          Mi.data_ptr() if Mi is not None else 0,
                          Li.data_ptr() if Li is not None else 0,

@@ -106,8 +106,8 @@ def test_paged_output_formats():
 
 def test_python_entries_reject_buffers_the_kernels_would_overrun():
     """A caller's O must match the shape and element size the kernels write
-    (O defaults to fp32), and a caller's workspace must be a device buffer:
-    anything else raises before any launch."""
+    (O defaults to fp32), a caller's workspace must be a device buffer and
+    key counts must be contiguous: anything else raises before any launch."""
     import pytest
     import torch
 
@@ -130,6 +130,14 @@ def test_python_entries_reject_buffers_the_kernels_would_overrun():
     assert kf.plan(1, 1, 4096, 4, 2, 64).workspace_bytes > 0
     with pytest.raises(ValueError):
         kf.attn_fwd(Q1, K1, K1, workspace=torch.empty(1 << 24, dtype=torch.uint8))
+    # Key counts are read in the caller's layout: a strided view is rejected
+    # (a copy made on another stream would be unordered with the launch).
+    Q2 = torch.zeros((2, 4, 8, 64), dtype=torch.float16, device=dev)
+    K2 = torch.zeros((2, 2, 16, 64), dtype=torch.float16, device=dev)
+    strided = torch.full((4,), 8, dtype=torch.int32, device=dev)[::2]
+    assert not strided.is_contiguous()
+    with pytest.raises(ValueError):
+        kf.attn_fwd(Q2, K2, K2, kv_lens=strided)
     # Paged decode: same rule for O.
     Kp = torch.zeros((8, 2, 16, 64), dtype=torch.float16, device=dev)
     table = torch.arange(8, dtype=torch.int32, device=dev).reshape(1, 8)
