@@ -219,12 +219,21 @@ def _out_flags(torch, out_dtype, return_lse):
     return f[out_dtype] | (KF_ATTN_LSE if return_lse else 0)
 
 
-def _output(torch, out, shape, out_dtype, device):
+def _new(torch, shape, dtype, device, stream):
+    """A new tensor written on ``stream``: torch allocates it for its current
+    stream, so ``stream`` is recorded, and the memory is not handed out again
+    before the launch on ``stream`` has finished with it."""
+    t = torch.empty(shape, dtype=dtype, device=device)
+    t.record_stream(stream)
+    return t
+
+
+def _output(torch, out, shape, out_dtype, device, stream):
     """The output tensor: a new one, or the caller's after checking that the
     kernel's writes (shape x element size of ``out_dtype``) land inside it."""
     dtype = out_dtype or torch.float32
     if out is None:
-        return torch.empty(shape, dtype=dtype, device=device)
+        return _new(torch, shape, dtype, device, stream)
     if out.dtype != dtype or tuple(out.shape) != tuple(shape) or out.device != device \
             or not out.is_contiguous():
         raise ValueError(f"out must be a contiguous {dtype} tensor of shape {tuple(shape)} "
@@ -242,9 +251,7 @@ def _workspace(torch, workspace, need, device, stream):
             raise ValueError(f"workspace must be a contiguous tensor on {device}")
         if workspace.numel() * workspace.element_size() >= need:
             return workspace
-    workspace = torch.empty(need, dtype=torch.uint8, device=device)
-    workspace.record_stream(stream)
-    return workspace
+    return _new(torch, need, torch.uint8, device, stream)
 
 
 def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=None,
@@ -277,15 +284,15 @@ def attn_fwd(Q, K, V, out=None, *, return_stats=False, workspace=None, stream=No
     Bk, H_kv, kv_len, Dk = K.shape
     if Bk != B or Dk != D:
         raise ValueError("Q and K/V disagree on B or D")
-    out = _output(torch, out, (B, H_q, q_len, D), out_dtype, Q.device)
-    Mi = Li = None
-    if return_stats or return_lse:
-        Mi = torch.empty((B, H_q, q_len), dtype=torch.float32, device=Q.device)
-    if return_stats:
-        Li = torch.empty_like(Mi)
-    need = workspace_bytes(B, q_len, kv_len, H_q, H_kv, D)
     if stream is None:
         stream = torch.cuda.current_stream(Q.device)
+    out = _output(torch, out, (B, H_q, q_len, D), out_dtype, Q.device, stream)
+    Mi = Li = None
+    if return_stats or return_lse:
+        Mi = _new(torch, (B, H_q, q_len), torch.float32, Q.device, stream)
+    if return_stats:
+        Li = _new(torch, (B, H_q, q_len), torch.float32, Q.device, stream)
+    need = workspace_bytes(B, q_len, kv_len, H_q, H_kv, D)
     workspace = _workspace(torch, workspace, need, Q.device, stream)
     if kv_lens is not None:
         # A contiguous copy would be made on torch's current stream, unordered
@@ -343,15 +350,15 @@ def attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, out=None, *, re
     if block_table.dim() != 2 or block_table.shape[0] != B or kv_lens.numel() != B:
         raise ValueError("block_table must be [B, max_pages_per_seq] and kv_lens [B]")
     max_pages = block_table.shape[1]
-    out = _output(torch, out, (B, H_q, q_len, D), out_dtype, Q.device)
-    Mi = Li = None
-    if return_stats or return_lse:
-        Mi = torch.empty((B, H_q, q_len), dtype=torch.float32, device=Q.device)
-    if return_stats:
-        Li = torch.empty_like(Mi)
-    need = paged_workspace_bytes(B, q_len, H_q, H_kv, D, page_size, max_pages)
     if stream is None:
         stream = torch.cuda.current_stream(Q.device)
+    out = _output(torch, out, (B, H_q, q_len, D), out_dtype, Q.device, stream)
+    Mi = Li = None
+    if return_stats or return_lse:
+        Mi = _new(torch, (B, H_q, q_len), torch.float32, Q.device, stream)
+    if return_stats:
+        Li = _new(torch, (B, H_q, q_len), torch.float32, Q.device, stream)
+    need = paged_workspace_bytes(B, q_len, H_q, H_kv, D, page_size, max_pages)
     workspace = _workspace(torch, workspace, need, Q.device, stream)
     st = attn_decode_paged_ptr(Q.data_ptr(), K_pages.data_ptr(), V_pages.data_ptr(),
                                block_table.data_ptr(), kv_lens.data_ptr(), out.data_ptr(),

@@ -150,3 +150,34 @@ def test_python_entries_reject_buffers_the_kernels_would_overrun():
     O16 = kf.attn_decode_paged(Q1, Kp, Kp, table, lens, out_dtype=torch.float16)
     torch.cuda.synchronize()
     assert torch.isfinite(O).all() and O16.dtype == torch.float16
+
+
+def test_python_entries_on_a_side_stream():
+    """attn_fwd / attn_decode_paged launched on a stream other than torch's
+    current one (new O, Mi, Li and workspace allocated by the call) give the
+    same bits as on the current stream."""
+    import torch
+
+    import kernelfoundry_amd as kf
+
+    _announce(test="side_stream")
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(5)
+    Q = torch.randn((2, 32, 1, 128), generator=g, device=dev).half()
+    K = torch.randn((2, 8, 3000, 128), generator=g, device=dev).half()
+    V = torch.randn((2, 8, 3000, 128), generator=g, device=dev).half()
+    assert kf.plan(2, 1, 3000, 32, 8, 128).workspace_bytes > 0
+    Kp = K[0].reshape(8, 3000 // 24, 24, 128)[:, :120, :16].permute(1, 0, 2, 3).contiguous()
+    Vp = V[0].reshape(8, 3000 // 24, 24, 128)[:, :120, :16].permute(1, 0, 2, 3).contiguous()
+    table = torch.arange(120, dtype=torch.int32, device=dev).flip(0).reshape(2, 60).contiguous()
+    lens = torch.tensor([960, 513], dtype=torch.int32, device=dev)
+    ref = kf.attn_fwd(Q, K, V, return_stats=True)
+    ref_p = kf.attn_decode_paged(Q, Kp, Vp, table, lens, return_stats=True)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    got = kf.attn_fwd(Q, K, V, return_stats=True, stream=side)
+    got_p = kf.attn_decode_paged(Q, Kp, Vp, table, lens, return_stats=True, stream=side)
+    side.synchronize()
+    for a, b in zip(ref + ref_p, got + got_p):
+        assert torch.equal(a, b)
