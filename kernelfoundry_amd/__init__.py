@@ -220,12 +220,15 @@ def _out_flags(torch, out_dtype, return_lse):
 
 
 def _new(torch, shape, dtype, device, stream):
-    """A new tensor written on ``stream``: torch allocates it for its current
-    stream, so ``stream`` is recorded, and the memory is not handed out again
-    before the launch on ``stream`` has finished with it."""
-    t = torch.empty(shape, dtype=dtype, device=device)
-    t.record_stream(stream)
-    return t
+    """A new tensor written on ``stream``, allocated from ``stream``'s pool of
+    torch's caching allocator.  A block of that pool was last used by work on
+    ``stream`` itself, so the launch that follows on ``stream`` is ordered
+    after that work; a block taken from another stream's pool (torch's
+    current one) could still be in use by a kernel queued there.  Freed, the
+    tensor returns to ``stream``'s pool, so it is not reused before the
+    launch on ``stream`` has finished with it."""
+    with torch.cuda.stream(stream):
+        return torch.empty(shape, dtype=dtype, device=device)
 
 
 def _output(torch, out, shape, out_dtype, device, stream):

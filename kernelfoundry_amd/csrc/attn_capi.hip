@@ -333,6 +333,10 @@ int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const 
     prm.heads_kv = H_kv;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
+    // Launch errors are read back with hipGetLastError(); clear whatever an
+    // earlier, unrelated HIP call on this thread left there first, so that
+    // only this call's own launches decide its status.
+    (void)hipGetLastError();
     hipError_t e;
     switch (D) {
         case 16: e = launch_all<16>(pl, prm, s); break;

@@ -44,7 +44,9 @@ the tests live in tests/test_oracle.py):
                        Q=0 -> column means of V; one dominant score -> that V
                        row), invariants (GQA == MHA with repeat_interleave'd
                        K/V; joint permutation of K/V rows; convex-combination
-                       bounds), and the committed golden fixtures.
+                       bounds).  The reference ships no fixture files; its
+                       one known-answer test (kernel_models/flash_attn.py:
+                       269-281) is reproduced for tiled_online_softmax below.
   * tiled_online_softmax -- equals sdpa on the reference's own smoke shapes
                        (kernel_models/flash_attn.py:269-281: B=1, S=16, H_q=2,
                        H_kv=1, D in {16,64,128}, max-abs < 1e-4) and on ragged

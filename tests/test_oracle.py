@@ -4,8 +4,9 @@ CPU only.  Each function of oracle/attn_oracle.py is checked against an
 independent computation -- a brute-force C triple loop (oracle/cpu_attn.c,
 restating tests/test_flash_attn.cu:119-169), torch's CPU
 scaled_dot_product_attention in fp64, libstdc++'s own RNG, closed forms,
-invariants and the committed golden fixtures -- and planted mistakes in the
-oracle are shown to fail those checks.
+invariants and the reference's own known-answer smoke test
+(kernel_models/flash_attn.py:269-281; the reference ships no fixture files)
+-- and planted mistakes in the oracle are shown to fail those checks.
 """
 import os
 import subprocess

@@ -181,3 +181,40 @@ def test_python_entries_on_a_side_stream():
     side.synchronize()
     for a, b in zip(ref + ref_p, got + got_p):
         assert torch.equal(a, b)
+
+
+def test_side_stream_outputs_do_not_reuse_memory_busy_on_the_current_stream():
+    """A tensor freed while a kernel queued on torch's current stream still
+    writes it must not become the O of a launch on another stream: the call
+    allocates O, Mi, Li and the workspace from the launch stream's pool.
+    The current stream is held busy (a spin kernel) in front of a fill of a
+    freed tensor of O's size; the side-stream result must equal the
+    current-stream result bit for bit."""
+    import torch
+
+    import kernelfoundry_amd as kf
+
+    _announce(test="side_stream_alloc")
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(9)
+    Q = torch.randn((1, 32, 1, 128), generator=g, device=dev).half()
+    K = torch.randn((1, 8, 4096, 128), generator=g, device=dev).half()
+    V = torch.randn((1, 8, 4096, 128), generator=g, device=dev).half()
+    assert kf.plan(1, 1, 4096, 32, 8, 128).workspace_bytes > 0
+    ref, ref_m, ref_l = kf.attn_fwd(Q, K, V, return_stats=True)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=dev)
+    cur = torch.cuda.current_stream(dev)
+    for _ in range(3):
+        X = torch.empty_like(ref)
+        Xm = torch.empty_like(ref_m)
+        Xw = torch.empty(kf.workspace_bytes(1, 1, 4096, 32, 8, 128), dtype=torch.uint8, device=dev)
+        torch.cuda._sleep(20_000_000)       # keeps the current stream busy for ~10 ms
+        X.fill_(7.0)
+        Xm.fill_(7.0)
+        Xw.fill_(7)
+        del X, Xm, Xw                        # freed to the current stream's pool, still pending
+        got, got_m, got_l = kf.attn_fwd(Q, K, V, return_stats=True, stream=side)
+        side.synchronize()
+        cur.synchronize()
+        assert torch.equal(got, ref) and torch.equal(got_m, ref_m) and torch.equal(got_l, ref_l)
