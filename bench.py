@@ -23,6 +23,15 @@ half of the metric):
                      pool twice the needed size (the reference's worst-case
                      fragmentation, bench_flash_attn2.py:153-215); bytes =
                      configs[4]'s plus the block table.
+  * ``decode.floor`` -- beside configs[1]: a bare read of the same K/V bytes
+                     over the same rotated sets (kf_probe_read) and an empty
+                     back-to-back dispatch (one kernel boundary), timed the
+                     same way; ``decode.graph``: the same steps replayed from
+                     one captured HIP graph.
+  * ``decode_sweep`` -- the reference bench's decode shapes (B=1 KV=512..4096,
+                     B=8 KV=512/1024, MQA KV=512/1024; tests/bench_flash_attn.cu:
+                     154-159, 181-182), each rotated over > 512 MB of sets,
+                     with the same read floor.
   * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep),
                      the MQA D=64 configs[3] and the configs[2] shape at
                      D=256 (the reference's largest head dimension).
@@ -32,7 +41,12 @@ FLOPs = 4*B*H_q*q_len*kv_len*D and bytes = fp16 Q + unique fp16 K,V + fp32 O
 the kernel's average duration measured here with HIP events around each
 launch on the launch stream.  ``cpu_baseline`` times the repo's NumPy
 restatement of the reference's CPU path (kernel_models/flash_attn.py:250-265)
-on a bounded sample of the same workload on this host's cores.
+on a bounded sample of the same workload on this host's cores;
+``cpu_baseline_c1_tiled`` times the restated tiled online-softmax model
+(kernel_models/flash_attn.py:184-246) on configs[0], the configuration
+BASELINE.json says runs on CPU.  ``roofline.kernel`` is the plan's kernel
+(kf_attn_kernel_names) and ``roofline.traffic`` the committed FETCH/WRITE
+figure only when it was collected on the current kernel sources.
 
 Timing protocol per workload: ``SETTLE_S`` seconds of untimed launches (the
 clocks reach their loaded steady state), W untimed warmup steps, then K timed
@@ -44,6 +58,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 from __future__ import annotations
 
 import argparse
+import ctypes
+import hashlib
 import json
 import math
 import os
@@ -60,6 +76,44 @@ PEAK_FP16_TFLOPS = 2516.6   # MI355X dense fp16 MFMA: 256 CU x 4096 FLOP/clk x 2
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 REF_PREFILL_S4096_TFLOPS = 19.3   # reference, RTX 5070 (README.md:49)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_prefill_s4096.json")
+PROBE_LIB = os.path.join(REPO, "kernelfoundry_amd", "lib", "libkf_probe.so")
+# The sources the prefill kernel and its launch plan are built from; the
+# committed FETCH/WRITE figures hold only for the sources they were collected on.
+KERNEL_SOURCES = ("kernelfoundry_amd/csrc/attn_kernels.h", "kernelfoundry_amd/csrc/attn_capi.hip")
+
+
+def source_sha256():
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(REPO, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def committed_traffic():
+    """(HBM bytes per launch, note) from profiles/traffic_prefill_s4096.json,
+    or (None, reason) when that file was collected on other kernel sources."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None, "no committed FETCH_SIZE / WRITE_SIZE collection"
+    with open(TRAFFIC_FILE) as f:
+        t = json.load(f)
+    if t.get("source_sha256") != source_sha256():
+        return None, ("stale: profiles/traffic_prefill_s4096.json was collected on other "
+                      "kernel sources (source_sha256 differs); re-collect FETCH_SIZE / WRITE_SIZE")
+    return t.get("traffic_bytes_per_launch"), "rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1 (calibrated)"
+
+
+def load_probe(kf):
+    """libkf_probe.so (include/kf/probe.h), loaded after the attention library
+    so that both bind to torch's HIP runtime."""
+    kf.load_library()
+    lib = ctypes.CDLL(PROBE_LIB)
+    p, sz = ctypes.c_void_p, ctypes.c_size_t
+    lib.kf_probe_read.argtypes = [p, p, sz, p, p]
+    lib.kf_probe_read.restype = ctypes.c_int
+    lib.kf_probe_empty.argtypes = [p]
+    lib.kf_probe_empty.restype = ctypes.c_int
+    return lib
 
 
 def flops(B, H_q, q, kv, D):
@@ -105,22 +159,23 @@ class Runner:
         self.lib = kf.load_library()
         self.i = 0
 
-    def launch(self):
+    def launch(self, stream=None):
         j = self.i % len(self.sets)
         self.i += 1
         Q, K, V = self.sets[j]
         B, q, kv, H_q, H_kv, D = self.shape
+        cs = (stream or self.stream).cuda_stream
         if self.flags:
             st = self.lib.kf_attn_fwd_ex(Q.data_ptr(), K.data_ptr(), V.data_ptr(),
                                          self.outs[j].data_ptr(), None, None, B, q, kv, H_q, H_kv,
                                          D, None, self.flags,
                                          self.ws.data_ptr() if self.ws_bytes else None,
-                                         self.ws_bytes, self.stream.cuda_stream)
+                                         self.ws_bytes, cs)
         else:
             st = self.lib.kf_attn_fwd(Q.data_ptr(), K.data_ptr(), V.data_ptr(),
                                       self.outs[j].data_ptr(), None, None, B, q, kv, H_q, H_kv, D,
                                       self.ws.data_ptr() if self.ws_bytes else None,
-                                      self.ws_bytes, self.stream.cuda_stream)
+                                      self.ws_bytes, cs)
         if st != 0:
             raise RuntimeError(f"kf_attn_fwd failed: {self.kf.status_string(st)}")
         return j
@@ -254,6 +309,138 @@ def run_paged_decode(torch, kf, steps, warmup, check, B=32, kv=8192, H_q=32, H_k
     return out
 
 
+class ProbeRunner:
+    """Back-to-back launches of a probe (same interface as Runner)."""
+
+    def __init__(self, torch, fn, n_sets=1):
+        self.stream = torch.cuda.current_stream()
+        self.fn, self.n, self.i = fn, n_sets, 0
+
+    def launch(self, stream=None):
+        j = self.i % self.n
+        self.i += 1
+        st = self.fn(j, (stream or self.stream).cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"probe launch failed ({st})")
+
+
+def decode_floors(torch, probe, sets, steps, warmup):
+    """Floors of a small decode step, timed like the step itself: a bare read
+    of the same K and V bytes (the same rotated sets) and an empty dispatch.
+    Back to back on one stream, the empty dispatch is the cost of a kernel
+    boundary."""
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    nbytes_kv = sets[0][1].numel() * 2
+
+    def read(j, cs):
+        return probe.kf_probe_read(sets[j][1].data_ptr(), sets[j][2].data_ptr(), nbytes_kv,
+                                   sink.data_ptr(), cs)
+
+    ms_read, _, _ = time_steps(torch, ProbeRunner(torch, read, len(sets)), steps, warmup)
+    ms_empty, _, _ = time_steps(torch, ProbeRunner(torch, lambda j, cs: probe.kf_probe_empty(cs)),
+                                steps, warmup)
+    return ms_read * 1e3, ms_empty * 1e3, 2.0 * nbytes_kv
+
+
+def time_graph(torch, runner, replays=20):
+    """The decode steps of one pass over the rotated sets captured into one
+    HIP graph (torch.cuda.CUDAGraph) and replayed back to back: per-step time,
+    and whether every replay reproduced the eager outputs bit for bit.  The
+    kernels record no memset, so the graph holds only their launches."""
+    n = len(runner.sets)
+    runner.i = 0
+    for _ in range(n):
+        runner.launch()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in runner.outs]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        runner.i = 0
+        for _ in range(n):
+            runner.launch(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    ok = True
+    for o in runner.outs:
+        o.zero_()
+    for _ in range(2):  # replays with eager work and syncs between them
+        g.replay()
+        torch.cuda.synchronize()
+        ok = ok and all(torch.equal(a, b) for a, b in zip(runner.outs, eager))
+        for o in runner.outs:
+            o.zero_()
+        torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(replays):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ok = ok and all(torch.equal(a, b) for a, b in zip(runner.outs, eager))
+    del g
+    return t0.elapsed_time(t1) / (replays * n) * 1e3, ok
+
+
+def cpu_baseline_tiled_c1(min_runs=3):
+    """configs[0] as BASELINE.json states it, "on CPU via the NumPy reference
+    model": the repo's restatement of the reference's tiled online-softmax
+    model (oracle.tiled_online_softmax = kernel_models/flash_attn.py:184-246,
+    Br=16, Bc_col=8, kv_block_rows=128, the k/co loops as row matmuls) on the
+    whole C1 prefill (S=512, 32/8 heads, D=128), median of the timed runs."""
+    import numpy as np
+
+    from oracle import attn_oracle as orc
+
+    S, D, H_q, H_kv = 512, 128, 32, 8
+    q, k, v = orc.normal_fp16_inputs(1, H_q, H_kv, S, S, D, 0)
+    q, k, v = q.astype(np.float32), k.astype(np.float32), v.astype(np.float32)
+    orc.tiled_online_softmax(q[:, :4], k[:, :1], v[:, :1])  # warm-up
+    runs = []
+    while len(runs) < min_runs:
+        t = time.perf_counter()
+        orc.tiled_online_softmax(q, k, v)
+        runs.append(time.perf_counter() - t)
+    sec = statistics.median(runs)
+    cores, threads, blas, cpu_model = host_info()
+    return {
+        "value": round(flops(1, H_q, S, S, D) / sec / 1e12, 5), "unit": "TFLOPS",
+        "cores": int(threads) if threads and threads.isdigit() else cores,
+        "kind": "port",
+        "sample": (f"configs[0] prefill S=512 GQA 32/8 D=128, all 32 heads, tiled online-softmax "
+                   f"model (oracle.tiled_online_softmax = kernel_models/flash_attn.py:184-246), "
+                   f"median of {len(runs)} runs = {sec:.2f} s; cpu '{cpu_model}', affinity "
+                   f"{cores} cores, BLAS {blas}, BLAS threads {threads or 'default'}"),
+    }
+
+
+def host_info():
+    import numpy as np
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    threads = os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS")
+    blas = "unknown"
+    try:
+        info = np.show_config(mode="dicts")["Build Dependencies"]["blas"]
+        blas = f"{info.get('name', '?')} {info.get('version', '')}".strip()
+    except Exception:  # older numpy: no dict form
+        pass
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return cores, threads, blas, cpu_model
+
+
 def cpu_baseline(seconds_target=12.0):
     """Time the NumPy restatement of the reference's CPU path (fp32 SDPA per
     head) on a bounded sample of the headline workload: up to all 32 query
@@ -282,26 +469,7 @@ def cpu_baseline(seconds_target=12.0):
         runs.append(time.perf_counter() - t)
     sec = statistics.median(runs)
     tflops = flops(1, n_heads, S, S, D) / sec / 1e12
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count()
-    threads = os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get("OMP_NUM_THREADS")
-    blas = "unknown"
-    try:
-        info = np.show_config(mode="dicts")["Build Dependencies"]["blas"]
-        blas = f"{info.get('name', '?')} {info.get('version', '')}".strip()
-    except Exception:  # older numpy: no dict form
-        pass
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    cores, threads, blas, cpu_model = host_info()
     return {
         "value": round(tflops, 4), "unit": "TFLOPS",
         "cores": int(threads) if threads and threads.isdigit() else cores,
@@ -412,6 +580,26 @@ def main():
         if args.only:
             return
         results["decode"]["parity"] = parity_spot_check(torch, rdec, [(0, 0), (0, 17)])
+        probe = load_probe(kf)
+        print("bench: decode floors and graph replay", file=sys.stderr, flush=True)
+        read_us, empty_us, read_bytes = decode_floors(torch, probe, rdec.sets, steps, warmup)
+        results["decode"]["floor"] = {
+            "read_us": round(read_us, 3),
+            "read_gbs": round(read_bytes / (read_us * 1e3), 1),
+            "read_bytes": read_bytes,
+            "boundary_us": round(empty_us, 3),
+            "note": ("read_us: kf_probe_read of the same K and V bytes over the same rotated sets, "
+                     "timed back to back like the decode step (one launch, one round trip per "
+                     "lane, no compute); boundary_us: an empty dispatch back to back, the cost of "
+                     "one kernel boundary on the stream; the split decode step is two launches"),
+        }
+        try:
+            g_us, g_ok = time_graph(torch, rdec)
+            results["decode"]["graph"] = {"step_us": round(g_us, 3), "replays_bitwise_equal": g_ok,
+                                          "note": "one pass over the rotated sets captured in one "
+                                                  "HIP graph, replayed back to back"}
+        except Exception as e:  # capture unsupported: report, keep the eager figures
+            results["decode"]["graph"] = {"step_us": None, "error": str(e)[:200]}
         del rdec
     if args.only in (None, "decode_b32"):
         print("bench: decode B=32 KV=8192", file=sys.stderr, flush=True)
@@ -427,6 +615,27 @@ def main():
         if args.only:
             return
 
+    print("bench: decode sweep", file=sys.stderr, flush=True)
+    probe = load_probe(kf)
+    decode_sweep = []
+    # The reference bench's decode shapes (tests/bench_flash_attn.cu:154-159,
+    # 181-182), each rotated over > 512 MB of distinct Q/K/V sets so that a
+    # step reads HBM, not the Infinity Cache copy of an earlier step.
+    for (B, kv, H_kv) in ((1, 512, 8), (1, 1024, 8), (1, 2048, 8), (1, 4096, 8), (8, 512, 8),
+                          (8, 1024, 8), (1, 512, 1), (1, 1024, 1)):
+        by = nbytes(B, 32, H_kv, 1, kv, 128)
+        n_sets = int(min(4000, math.ceil(600e6 / by)))
+        d, r = run_decode(B, kv, n_sets, D=128, H_kv=H_kv)
+        read_us, empty_us, _ = decode_floors(torch, probe, r.sets, steps, warmup)
+        decode_sweep.append({
+            "B": B, "H_q": 32, "H_kv": H_kv, "D": 128, "kv_len": kv, "sets_rotated": n_sets,
+            "latency_us": round(d["latency_us"], 3), "hbm_gbs": round(d["gbs"], 1),
+            "frac": round(d["gbs"] / PEAK_HBM_GBS, 4), "bytes": by,
+            "floor_read_us": round(read_us, 3), "boundary_us": round(empty_us, 3),
+            "kernels": kf.kernel_names(B, 1, kv, 32, H_kv, 128)})
+        del r
+        torch.cuda.empty_cache()
+
     print("bench: sweep", file=sys.stderr, flush=True)
     sweep = [run_prefill(S) for S in (512, 1024, 2048)]
     sweep.append(run_prefill(2048, H_kv=1, D=64))
@@ -440,10 +649,7 @@ def main():
     pre = results["prefill"]
     dec = results["decode"]
     b32 = results["decode_b32"]
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("traffic_bytes_per_launch")
+    traffic, traffic_note = committed_traffic()
 
     line = {
         "metric": METRIC,
@@ -464,12 +670,14 @@ def main():
                    "baseline_config": "configs[2]"},
         "roofline": {
             "bound": "mfma",
-            "kernel": "kf_attn_prefill_kernel<128, false, 8, 1>",
+            "kernel": kf.kernel_names(1, 4096, 4096, 32, 8, 128),
             "achieved": round(pre["kernel_tflops"], 2),
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(pre["kernel_tflops"] / PEAK_FP16_TFLOPS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_note,
+            "kernel_sources_sha256": source_sha256(),
             "algorithmic_flops_per_launch": flops(1, 32, 4096, 4096, 128),
             "kernel_ms_mean": round(pre["kernel_ms_mean"], 5),
         },
@@ -483,8 +691,12 @@ def main():
             "path": dec["path"], "splits": dec["splits"],
             "sets_rotated": dec["sets_rotated"],
             "launch_us_mean": round(dec["launch_us_mean"], 3),
+            "kernels": kf.kernel_names(1, 1, 4096, 32, 8, 128),
+            "floor": dec["floor"],
+            "graph": dec["graph"],
             "parity": dec["parity"],
         },
+        "decode_sweep": decode_sweep,
         "decode_b32": {
             "config": "configs[4]: B=32 H_q=32 H_kv=8 D=128 q_len=1 kv_len=8192",
             "latency_us": round(b32["latency_us"], 2),
@@ -503,6 +715,8 @@ def main():
     if not args.no_cpu_baseline:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline()
+        print("bench: cpu baseline, tiled model at configs[0]", file=sys.stderr, flush=True)
+        line["cpu_baseline_c1_tiled"] = cpu_baseline_tiled_c1()
     print(json.dumps(line), flush=True)
 
 

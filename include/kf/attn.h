@@ -81,10 +81,34 @@ typedef struct kf_attn_plan_t {
                               1 = the streaming decode kernel); 0 on prefill    */
 } kf_attn_plan_t;
 
-/* Describe the dispatch kf_attn_fwd would use.  Validates like kf_attn_fwd
- * (sizes only, no pointers) and touches no GPU state. */
+/* Describe the dispatch kf_attn_fwd would use on the device current on the
+ * calling thread.  Validates like kf_attn_fwd (sizes only, no pointers).
+ * The plan is sized for that device's compute units and XCDs, read once per
+ * device with hipDeviceGetAttribute (the reference's launcher likewise sizes
+ * its launch from the device, tests/test_flash_attn.cu:28-48); without a
+ * visible device it is the plan for a whole MI355X (256 CUs, 8 XCDs).
+ * kf_attn_fwd, kf_attn_fwd_ex, kf_attn_decode_paged and the workspace
+ * queries plan the same way, so a workspace sized on the current device fits
+ * calls on streams of that device. */
 int kf_attn_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
                  kf_attn_plan_t* plan);
+
+/* The plan for a device with num_cus compute units (no device query; for
+ * planning ahead and for host-only tests).  No reference counterpart.
+ * num_cus <= 0 -> KF_ERR_SIZE. */
+int kf_attn_plan_for_cus(int B, int q_len, int kv_len, int H_q, int H_kv, int D, int num_cus,
+                         kf_attn_plan_t* plan);
+
+/* Names of the kernels kf_attn_fwd_ex launches for this shape on the current
+ * device, in launch order and as a profiler lists them, e.g.
+ * "kf_attn_prefill_kernel<128, false, 8, 1>" or
+ * "kf_attn_decode_short_kernel<128, 1> + kf_attn_split_merge_kernel<128, 8, 4>";
+ * `flags` (KF_ATTN_CAUSAL) and whether kv_lens is non-NULL (never read) pick
+ * the masked prefill.  NUL-terminated into buf; KF_ERR_SIZE if buf_bytes is
+ * too small.  No reference counterpart (its launchers print the launch
+ * geometry, tests/test_flash_attn.cu:86-91). */
+int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D, int flags,
+                         const int* kv_lens, char* buf, size_t buf_bytes);
 
 /* Bytes of device workspace kf_attn_fwd needs for this shape (0 when the
  * shape runs without split-KV partials).  Returns 0 for invalid shapes too;

@@ -21,7 +21,8 @@ Interface, mirroring the reference harness (sviraaj/kernelfoundry):
 * ``attn_decode_paged(Q, K_pages, V_pages, block_table, kv_lens, ...)`` --
   kf_attn_decode_paged: decode over a paged K/V cache (page pools
   [num_pages, H_kv, page_size, D] and a per-sequence block table).
-* ``plan(B, q_len, kv_len, H_q, H_kv, D)`` -- which kernels run, GPU-free.
+* ``plan(B, q_len, kv_len, H_q, H_kv, D, num_cus=None)`` -- which kernels run,
+  sized for the current device's compute units (or ``num_cus``).
 """
 from __future__ import annotations
 
@@ -34,10 +35,11 @@ __all__ = [
     "KfError", "LIB_PATH", "load_library", "plan", "workspace_bytes", "attn_fwd",
     "attn_fwd_ptr", "launch_flash_attn", "status_string", "exported_symbols",
     "KF_OK", "KF_ERR_HEAD_DIM", "KF_ERR_GQA", "KF_ERR_SIZE", "KF_ERR_NULL",
-    "KF_ERR_WORKSPACE", "KF_ERR_ALIGN", "KF_ERR_HIP", "KF_ERR_FLAGS", "KF_ATTN_CAUSAL",
+    "KF_ERR_WORKSPACE", "KF_ERR_ALIGN", "KF_ERR_HIP", "KF_ERR_FLAGS",
+    "KF_ATTN_CAUSAL",
     "KF_ATTN_OUT_F16", "KF_ATTN_OUT_BF16", "KF_ATTN_LSE",
     "PATH_NAMES", "attn_fwd_ex_ptr", "attn_decode_paged", "attn_decode_paged_ptr",
-    "paged_workspace_bytes",
+    "paged_workspace_bytes", "kernel_names",
 ]
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
@@ -130,8 +132,12 @@ def load_library(path: str = LIB_PATH):
     i, p, sz = ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
     lib.kf_attn_plan.argtypes = [i] * 6 + [ctypes.POINTER(_PlanStruct)]
     lib.kf_attn_plan.restype = i
+    lib.kf_attn_plan_for_cus.argtypes = [i] * 7 + [ctypes.POINTER(_PlanStruct)]
+    lib.kf_attn_plan_for_cus.restype = i
     lib.kf_attn_workspace_bytes.argtypes = [i] * 6
     lib.kf_attn_workspace_bytes.restype = sz
+    lib.kf_attn_kernel_names.argtypes = [i] * 7 + [p, ctypes.c_char_p, sz]
+    lib.kf_attn_kernel_names.restype = i
     lib.kf_attn_fwd.argtypes = [p, p, p, p, p, p] + [i] * 6 + [p, sz, p]
     lib.kf_attn_fwd.restype = i
     lib.kf_attn_fwd_ex.argtypes = [p, p, p, p, p, p] + [i] * 6 + [p, i, p, sz, p]
@@ -162,13 +168,32 @@ def status_string(status: int) -> str:
     return load_library().kf_status_string(int(status)).decode()
 
 
-def plan(B, q_len, kv_len, H_q, H_kv, D) -> Plan:
+def plan(B, q_len, kv_len, H_q, H_kv, D, num_cus=None) -> Plan:
+    """The dispatch for the current device (kf_attn_plan), or for a device
+    with ``num_cus`` compute units (kf_attn_plan_for_cus)."""
     out = _PlanStruct()
-    st = load_library().kf_attn_plan(B, q_len, kv_len, H_q, H_kv, D, ctypes.byref(out))
+    lib = load_library()
+    if num_cus is None:
+        st = lib.kf_attn_plan(B, q_len, kv_len, H_q, H_kv, D, ctypes.byref(out))
+    else:
+        st = lib.kf_attn_plan_for_cus(B, q_len, kv_len, H_q, H_kv, D, int(num_cus),
+                                      ctypes.byref(out))
     if st != KF_OK:
         raise KfError(st, status_string(st))
     return Plan(PATH_NAMES[out.path], out.rows_per_group, out.num_splits, out.kv_per_split,
                 out.grid_blocks, out.block_threads, int(out.workspace_bytes), out.splits_per_block)
+
+
+def kernel_names(B, q_len, kv_len, H_q, H_kv, D, causal=False, masked=False) -> str:
+    """The kernels kf_attn_fwd_ex runs for this shape on the current device,
+    as a profiler names them (``masked``: a kv_lens array is passed)."""
+    buf = ctypes.create_string_buffer(256)
+    st = load_library().kf_attn_kernel_names(B, q_len, kv_len, H_q, H_kv, D,
+                                             KF_ATTN_CAUSAL if causal else 0,
+                                             1 if masked else None, buf, len(buf))
+    if st != KF_OK:
+        raise KfError(st, status_string(st))
+    return buf.value.decode()
 
 
 def workspace_bytes(B, q_len, kv_len, H_q, H_kv, D) -> int:

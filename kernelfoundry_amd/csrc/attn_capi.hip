@@ -5,15 +5,23 @@
 // CPU-only tests rely on that) and never reach a kernel.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cstdint>
+#include <cstdio>
+#include <cstring>
 
 #include "attn_kernels.h"
 #include "kf/attn.h"
 
 namespace {
 
-constexpr int kNumCUs = 256;            // MI355X compute units
+// The dispatch plan is sized for the device's compute units and XCDs,
+// read once per device (hipDeviceGetAttribute).  Without a visible device
+// (plan queries on a host without a GPU) it plans for a whole MI355X.
+constexpr int kDefaultCUs = 256;        // MI355X in SPX mode
+constexpr int kDefaultXcds = 8;
+constexpr int kMaxDevices = 64;
 constexpr int kDecodeMaxRows = 32;      // query rows per KV head on the decode path
 // Streaming decode: a split holds at least one 32-key stage per wave.
 inline int decode_min_split_rows(int D) { return kf::decode_waves(D) * kf::kDecodeStage; }
@@ -25,13 +33,13 @@ inline int decode_min_split_rows(int D) { return kf::decode_waves(D) * kf::kDeco
 // splits = 3 full rounds, not 3 splits = 1 round plus a 32-workgroup tail).
 // D = 256 (4 waves; its LDS holds one workgroup per CU): grids of two
 // workgroups per CU, i.e. two rounds, which measured 3 % faster than one.
-long long decode_stream_splits(long long n_groups, long long max_splits, int D) {
-    if (D >= 256) return (2LL * kNumCUs + n_groups - 1) / n_groups;
-    const double even = (double)n_groups / kNumCUs;
+long long decode_stream_splits(long long n_groups, long long max_splits, int D, int cus) {
+    if (D >= 256) return (2LL * cus + n_groups - 1) / n_groups;
+    const double even = (double)n_groups / cus;
     long long best = 1;
     double best_t = 1e300;
     for (long long s = 1; s <= max_splits; ++s) {
-        const double t = (double)((n_groups * s + kNumCUs - 1) / kNumCUs) / (double)s;
+        const double t = (double)((n_groups * s + cus - 1) / cus) / (double)s;
         if (t <= even * 1.02) return s;
         if (t < best_t * 0.98) {
             best = s;
@@ -41,15 +49,45 @@ long long decode_stream_splits(long long n_groups, long long max_splits, int D) 
     return best;
 }
 // Short-split decode (one wave per split of 32 or 64 keys): used while the
-// job is at most kShortMaxWaves such waves (8 per CU); beyond it the work is
+// job is at most kShortMaxWavesPerCU such waves per CU; beyond it the work is
 // bandwidth-bound and the streaming decode kernel takes over.  64-key splits
-// are preferred while they still give kShortMinWaves waves (4 per CU).
-constexpr long long kShortMaxWaves = 8LL * kNumCUs;
-constexpr long long kShortMinWaves = 4LL * kNumCUs;
+// are preferred while they still give kShortMinWavesPerCU waves per CU.
+constexpr long long kShortMaxWavesPerCU = 8;
+constexpr long long kShortMinWavesPerCU = 4;
 constexpr int kMinGroupKeys = 128;      // keys before a prefill row's keys are split in two
 constexpr size_t kWsAlign = 256;
 
 thread_local int g_last_hip_error = 0;
+
+struct DeviceShape {
+    int cus;
+    int xcds;
+};
+
+// CU and XCD counts of the device current on the calling thread, cached per
+// device; the MI355X defaults when no device is visible.
+DeviceShape current_device_shape() {
+    static std::atomic<int> cache[kMaxDevices][2];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return {kDefaultCUs, kDefaultXcds};
+    }
+    int cus = cache[dev][0].load(std::memory_order_relaxed);
+    int xcds = cache[dev][1].load(std::memory_order_relaxed);
+    if (cus <= 0 || xcds <= 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = kDefaultCUs;
+        if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess ||
+            xcds <= 0)
+            xcds = kDefaultXcds;
+        (void)hipGetLastError();
+        cache[dev][0].store(cus, std::memory_order_relaxed);
+        cache[dev][1].store(xcds, std::memory_order_relaxed);
+    }
+    return {cus, xcds};
+}
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -72,12 +110,15 @@ struct Plan {
     int merge_per;      // split merge: splits per lane
     size_t ws_bytes;
     size_t ws_o_off, ws_m_off, ws_l_off;
+    int xcds;           // XCDs of the target device (workgroup id remap)
 };
 
 // paged: K/V come from a page pool (kf_attn_decode_paged), which only the
-// streaming decode kernel reads.
-int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl, bool paged = false) {
-    if (B <= 0 || q_len <= 0 || kv_len <= 0 || H_q <= 0 || H_kv <= 0) return KF_ERR_SIZE;
+// streaming decode kernel reads.  cus: compute units of the target device.
+int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const DeviceShape& dev,
+              Plan* pl, bool paged = false) {
+    const int cus = dev.cus;
+    if (B <= 0 || q_len <= 0 || kv_len <= 0 || H_q <= 0 || H_kv <= 0 || cus <= 0) return KF_ERR_SIZE;
     if (!supported_head_dim(D)) return KF_ERR_HEAD_DIM;
     if (H_q % H_kv != 0) return KF_ERR_GQA;
     const long long ratio = H_q / H_kv;
@@ -89,6 +130,7 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl, 
         return KF_ERR_SIZE;
 
     Plan p{};
+    p.xcds = dev.xcds;
     p.R = (int)R;
     p.n_groups = (int)n_groups;
     p.rows_total = (int)rows_total;
@@ -100,10 +142,10 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl, 
         if (!paged) {
             const auto waves = [&](int st) { return n_groups * ((kv_len + 32LL * st - 1) / (32LL * st)); };
             const auto fits = [&](int st) {
-                return st <= (D >= 256 ? 1 : 2) && waves(st) <= kShortMaxWaves &&
+                return st <= (D >= 256 ? 1 : 2) && waves(st) <= kShortMaxWavesPerCU * cus &&
                        (kv_len + 32LL * st - 1) / (32LL * st) <= kf::kMergeMaxSplits;
             };
-            if (fits(2) && waves(2) >= kShortMinWaves) nst = 2;
+            if (fits(2) && waves(2) >= kShortMinWavesPerCU * cus) nst = 2;
             else if (fits(1)) nst = 1;
             else if (fits(2)) nst = 2;
         }
@@ -117,7 +159,7 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl, 
             long long max_splits = kv_len / decode_min_split_rows(D);
             if (max_splits < 1) max_splits = 1;
             if (max_splits > kf::kMergeMaxSplits) max_splits = kf::kMergeMaxSplits;
-            splits = decode_stream_splits(n_groups, max_splits, D);
+            splits = decode_stream_splits(n_groups, max_splits, D, cus);
             if (splits > max_splits) splits = max_splits;
             if (splits > kf::kMergeMaxSplits) splits = kf::kMergeMaxSplits;
             if (splits < 1) splits = 1;
@@ -144,12 +186,12 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, Plan* pl, 
         // accumulators need a SIMD per wave).
         int nw = kf::prefill_max_waves(D), ks = 1;
         const auto wgs = [&](long long rows) { return n_groups * ((R + rows - 1) / rows); };
-        if ((D == 64 || D == 128) && wgs(32 * nw) < kNumCUs && kv_len >= kMinGroupKeys) {
+        if ((D == 64 || D == 128) && wgs(32 * nw) < cus && kv_len >= kMinGroupKeys) {
             ks = 2;
-            if (wgs(128) < kNumCUs) nw = 4;
+            if (wgs(128) < cus) nw = 4;
         } else {
             const int nw_min = D >= 256 ? 4 : 2;
-            while (nw > nw_min && wgs(32 * nw) < kNumCUs) nw /= 2;
+            while (nw > nw_min && wgs(32 * nw) < cus) nw /= 2;
         }
         const int rows = 32 * nw / ks;
         const long long row_tiles = (R + rows - 1) / rows;
@@ -331,6 +373,7 @@ int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const 
     prm.causal = (flags & KF_ATTN_CAUSAL) ? 1 : 0;
     prm.q_len = q_len;
     prm.heads_kv = H_kv;
+    prm.xcds = pl.xcds;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     // Launch errors are read back with hipGetLastError(); clear whatever an
@@ -364,14 +407,11 @@ int paged_geometry(int page_size, int max_pages_per_seq, int num_pages, int* shi
     return KF_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int kf_attn_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, kf_attn_plan_t* plan) {
+int describe_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const DeviceShape& dev,
+                  kf_attn_plan_t* plan) {
     if (!plan) return KF_ERR_NULL;
     Plan pl;
-    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, &pl);
+    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, dev, &pl);
     if (st != KF_OK) return st;
     plan->path = pl.path;
     plan->rows_per_group = pl.R;
@@ -384,9 +424,49 @@ int kf_attn_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, kf_attn
     return KF_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
+int kf_attn_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, kf_attn_plan_t* plan) {
+    return describe_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), plan);
+}
+
+int kf_attn_plan_for_cus(int B, int q_len, int kv_len, int H_q, int H_kv, int D, int num_cus,
+                         kf_attn_plan_t* plan) {
+    if (num_cus <= 0) return KF_ERR_SIZE;
+    return describe_plan(B, q_len, kv_len, H_q, H_kv, D, DeviceShape{num_cus, kDefaultXcds}, plan);
+}
+
+int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D, int flags,
+                         const int* kv_lens, char* buf, size_t buf_bytes) {
+    if (!buf || buf_bytes == 0) return KF_ERR_NULL;
+    Plan pl;
+    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), &pl);
+    if (st != KF_OK) return st;
+    char tmp[192];
+    int n;
+    if (pl.path == KF_PATH_PREFILL) {
+        const bool mask = (flags & KF_ATTN_CAUSAL) || kv_lens;
+        n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_kernel<%d, %s, %d, %d>", D,
+                     mask ? "true" : "false", pl.waves, pl.kv_groups);
+    } else {
+        if (pl.short_stages > 0)
+            n = snprintf(tmp, sizeof(tmp), "kf_attn_decode_short_kernel<%d, %d>", D, pl.short_stages);
+        else
+            n = snprintf(tmp, sizeof(tmp), "kf_attn_decode_kernel<%d, false>", D);
+        if (pl.path == KF_PATH_DECODE_SPLIT)
+            n += snprintf(tmp + n, sizeof(tmp) - (size_t)n, " + kf_attn_split_merge_kernel<%d, %d, %d>", D,
+                          pl.merge_per, pl.merge_cw);
+    }
+    if (n < 0 || (size_t)n + 1 > buf_bytes) return KF_ERR_SIZE;
+    memcpy(buf, tmp, (size_t)n + 1);
+    return KF_OK;
+}
+
 size_t kf_attn_workspace_bytes(int B, int q_len, int kv_len, int H_q, int H_kv, int D) {
     Plan pl;
-    if (make_plan(B, q_len, kv_len, H_q, H_kv, D, &pl) != KF_OK) return 0;
+    if (make_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), &pl) != KF_OK) return 0;
     return pl.ws_bytes;
 }
 
@@ -402,7 +482,7 @@ int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, void* O, float* 
                    const int* kv_lens, int flags, void* workspace, size_t workspace_bytes,
                    void* stream) {
     Plan pl;
-    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, &pl);
+    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), &pl);
     if (st != KF_OK) return st;
     kf::AttnParams prm{};
     prm.kv_lens = kv_lens;
@@ -415,7 +495,8 @@ size_t kf_attn_decode_paged_workspace_bytes(int B, int q_len, int H_q, int H_kv,
     int sh, cap;
     if (paged_geometry(page_size, max_pages_per_seq, 1, &sh, &cap) != KF_OK) return 0;
     Plan pl;
-    if (make_plan(B, q_len, cap, H_q, H_kv, D, &pl, true) != KF_OK || pl.path == KF_PATH_PREFILL)
+    if (make_plan(B, q_len, cap, H_q, H_kv, D, current_device_shape(), &pl, true) != KF_OK ||
+        pl.path == KF_PATH_PREFILL)
         return 0;
     return pl.ws_bytes;
 }
@@ -429,7 +510,7 @@ int kf_attn_decode_paged(const void* Q, const void* K_pages, const void* V_pages
     int st = paged_geometry(page_size, max_pages_per_seq, num_pages, &sh, &cap);
     if (st != KF_OK) return st;
     Plan pl;
-    st = make_plan(B, q_len, cap, H_q, H_kv, D, &pl, true);
+    st = make_plan(B, q_len, cap, H_q, H_kv, D, current_device_shape(), &pl, true);
     if (st != KF_OK) return st;
     if (pl.path == KF_PATH_PREFILL) return KF_ERR_SIZE;  // more than 32 query rows per KV head
     if (!block_table || !kv_lens) return KF_ERR_NULL;
@@ -446,7 +527,8 @@ int kf_attn_decode_paged(const void* Q, const void* K_pages, const void* V_pages
 int kf_launch_flash_attn(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,
                          int B, int S, int H_q, int H_kv, int D, void* stream) {
     Plan pl;
-    if (make_plan(B, S, S, H_q, H_kv, D, &pl) != KF_OK) return (int)hipErrorInvalidValue;
+    if (make_plan(B, S, S, H_q, H_kv, D, current_device_shape(), &pl) != KF_OK)
+        return (int)hipErrorInvalidValue;
     if (!Q || !K || !V || !O || !aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
         return (int)hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);

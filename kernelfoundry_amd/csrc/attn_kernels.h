@@ -76,7 +76,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 // exceeds it by more than this many powers of two; P then stays <= 2^8,
 // exact in fp16's range, and most tiles skip the O rescale.
 constexpr float kLazyRescaleLog2 = 8.0f;
-constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
 
 // ---------------------------------------------------------------------------
 // Kernel parameter blocks (passed by value).
@@ -120,6 +119,9 @@ struct AttnParams {
     // Mi slot receives LSE = Mi + ln(Li) and Li is not written.
     int out_dtype;
     int lse;
+    // XCDs of the device (8 on an MI355X in SPX mode, 1 per CPX partition):
+    // the dispatcher deals workgroup ids round-robin over them.
+    int xcds;
 };
 
 enum : int { kOutF32 = 0, kOutF16 = 1, kOutBF16 = 2 };
@@ -261,10 +263,11 @@ __device__ __forceinline__ f16x8 as_f16x8(const u32x4& v) { return __builtin_bit
 
 // Hardware workgroup id -> logical id such that each XCD receives one
 // contiguous range of logical ids (the dispatcher deals ids round-robin over
-// the 8 XCDs).  Logical neighbours share K/V, so each XCD's L2 holds them.
-__device__ __forceinline__ int xcd_remap(int hw, int n) {
-    const int q = n / kXcds, r = n % kXcds;
-    const int xcd = hw % kXcds, k = hw / kXcds;
+// the nx XCDs).  Logical neighbours share K/V, so each XCD's L2 holds them.
+// A bijection on [0, n) for any nx >= 1 (nx = 1: the identity).
+__device__ __forceinline__ int xcd_remap(int hw, int n, int nx) {
+    const int q = n / nx, r = n % nx;
+    const int xcd = hw % nx, k = hw / nx;
     return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + k;
 }
 
@@ -768,7 +771,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const int wave = KS == 1 ? wave_id : wave_id % kRowWaves;  // row wave
     const int kgrp = KS == 1 ? 0 : wave_id / kRowWaves;        // KV group
     const int g = lane >> 5;
-    const int blk = xcd_remap(blockIdx.x, gridDim.x);
+    const int blk = xcd_remap(blockIdx.x, gridDim.x, p.xcds);
     int rt = blk % p.row_tiles;
     const int grp = blk / p.row_tiles;
     const int R = p.rows_per_group;
@@ -1247,7 +1250,7 @@ void kf_attn_decode_kernel(AttnParams p) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5;
-    const int blk = xcd_remap(blockIdx.x, gridDim.x);
+    const int blk = xcd_remap(blockIdx.x, gridDim.x, p.xcds);
     const int split = blk % p.n_splits;
     const int grp = blk / p.n_splits;
     const int R = p.rows_per_group;
@@ -1471,7 +1474,7 @@ void kf_attn_decode_short_kernel(AttnParams p) {
     const int row = lane & 31;
     const int R = p.rows_per_group;
     const int ns = p.n_splits;
-    const int wid = xcd_remap(blockIdx.x, gridDim.x) * kShortWaves + wave;
+    const int wid = xcd_remap(blockIdx.x, gridDim.x, p.xcds) * kShortWaves + wave;
     if (wid >= (p.rows_total / R) * ns) return;  // past the last split (wave-uniform)
     const int split = wid % ns, grp = wid / ns;
     const int kvb = batch_kv_len(p, grp);
@@ -1671,7 +1674,7 @@ void kf_attn_split_merge_kernel(AttnParams p) {
     constexpr int kNCB = (D / 4) / CW;             // column blocks per row
     constexpr int kSL = 64 / CW;                   // split lanes per column
     const int lane = threadIdx.x;
-    const int mb = xcd_remap(blockIdx.x, gridDim.x);
+    const int mb = xcd_remap(blockIdx.x, gridDim.x, p.xcds);
     const int row = mb / kNCB;                     // global query row
     const int cb = mb % kNCB;
     const int R = p.rows_per_group;

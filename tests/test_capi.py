@@ -266,6 +266,97 @@ def test_prefill_waves_per_workgroup(S, H_kv, D, waves, rows):
         assert rows == 32 * waves
 
 
+@pytest.mark.parametrize("cus", [32, 80, 256])
+def test_plans_scale_with_the_device_cu_count(cus):
+    """kf_attn_plan_for_cus sizes the dispatch for `cus` compute units: the
+    prefill splits rows between KV groups, and the decode uses short
+    one-wave splits, only while the plain grid would leave CUs idle; a
+    decode that fills the device streams with the fewest splits whose
+    busiest CU is within 2 % of an even share."""
+    # C1 prefill (S=512): 8 heads x 8 row tiles of 256 rows = 64 workgroups.
+    p = kf.plan(1, 512, 512, 32, 8, 128, num_cus=cus)
+    if 64 >= cus:
+        assert p.block_threads == 512 and p.grid_blocks == 64          # 8 waves, one KV group
+    elif 8 * (4 * 512 // 128) >= cus:
+        assert p.block_threads == 512 and p.grid_blocks == 128         # 2 KV groups, 128 rows
+    else:
+        assert p.block_threads == 256 and p.grid_blocks == 256         # 2 KV groups, 64 rows
+    # C3 prefill: 512 workgroups whatever the device.
+    assert kf.plan(1, 4096, 4096, 32, 8, 128, num_cus=cus).grid_blocks == 512
+    # C2 decode: short splits while 1024 one-wave splits fit 8 per CU.
+    p = kf.plan(1, 1, 4096, 32, 8, 128, num_cus=cus)
+    w64, w32 = 8 * 64, 8 * 128                   # waves of 64- and 32-key splits
+    if 4 * cus <= w64 <= 8 * cus:                # 64-key splits give 4 to 8 waves per CU
+        assert p.splits_per_block == 4 and p.kv_per_split == 64
+    elif w32 <= 8 * cus:
+        assert p.splits_per_block == 4 and p.kv_per_split == 32
+    else:
+        assert p.splits_per_block == 1
+    if cus == 32:
+        # 1024 one-wave splits would be 32 waves per CU: the streaming
+        # kernel, one workgroup per CU (8 heads x 4 splits).
+        assert p.splits_per_block == 1 and p.grid_blocks == 32 and p.num_splits == 4
+    # C5 decode: 256 heads; busiest CU within 2 % of an even share.
+    p = kf.plan(32, 1, 8192, 32, 8, 128, num_cus=cus)
+    rounds = -(-256 * p.num_splits // cus) / p.num_splits
+    assert rounds <= 256 / cus * 1.02 or p.num_splits == 1 and 256 % cus == 0
+    assert p.grid_blocks == 256 * p.num_splits
+
+
+def test_plan_without_a_visible_device_is_the_mi355x_plan():
+    """On a host without a GPU kf_attn_plan plans for a whole MI355X."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible: kf_attn_plan uses its CU count")
+    for shape in [(1, 4096, 4096, 32, 8, 128), (1, 512, 512, 32, 8, 128), (1, 1, 4096, 32, 8, 128),
+                  (32, 1, 8192, 32, 8, 128), (4, 1, 70000, 32, 8, 256)]:
+        assert kf.plan(*shape) == kf.plan(*shape, num_cus=256)
+
+
+def test_plan_for_cus_rejects_bad_counts(lib):
+    out = kf._PlanStruct()
+    assert lib.kf_attn_plan_for_cus(1, 1, 1, 1, 1, 128, 0, ctypes.byref(out)) == kf.KF_ERR_SIZE
+    assert lib.kf_attn_plan_for_cus(1, 1, 1, 1, 1, 128, -4, ctypes.byref(out)) == kf.KF_ERR_SIZE
+    assert lib.kf_attn_plan_for_cus(1, 1, 1, 1, 1, 128, 80, None) == kf.KF_ERR_NULL
+
+
+def test_kernel_names_follow_the_plan(lib):
+    """kf_attn_kernel_names names the kernels in launch order, as the
+    profiler lists them."""
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == \
+        "kf_attn_prefill_kernel<128, true, 8, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, masked=True) == \
+        "kf_attn_prefill_kernel<128, true, 8, 1>"
+    assert kf.kernel_names(1, 512, 512, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 4, 2>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_kernel<256, false, 4, 1>"
+    assert kf.kernel_names(1, 1, 4096, 32, 8, 128) == \
+        "kf_attn_decode_short_kernel<128, 1> + kf_attn_split_merge_kernel<128, 8, 4>"
+    assert kf.kernel_names(32, 1, 8192, 32, 8, 128) == "kf_attn_decode_kernel<128, false>"
+    buf = ctypes.create_string_buffer(8)
+    assert lib.kf_attn_kernel_names(1, 1, 4096, 32, 8, 128, 0, None, buf, 8) == kf.KF_ERR_SIZE
+    assert lib.kf_attn_kernel_names(1, 1, 4096, 32, 8, 128, 0, None, None, 8) == kf.KF_ERR_NULL
+    assert lib.kf_attn_kernel_names(1, 1, 4096, 32, 8, 100, 0, None, buf, 8) == kf.KF_ERR_HEAD_DIM
+
+
+def test_probe_library_exports_its_header():
+    """libkf_probe.so (bench.py's measurement probes) exports exactly what
+    include/kf/probe.h declares."""
+    lib_path = os.path.join(os.path.dirname(kf.LIB_PATH), "libkf_probe.so")
+    header = os.path.join(REPO, "include", "kf", "probe.h")
+    names = kf.exported_symbols(header)
+    assert set(names) == {"kf_probe_read", "kf_probe_empty"}
+    out = subprocess.run(["nm", "-D", "--defined-only", lib_path], capture_output=True,
+                         text=True, check=True).stdout
+    assert set(re.findall(r"\s[TW]\s+(kf_\w+)$", out, re.M)) == set(names)
+    kf.load_library()
+    probe = ctypes.CDLL(lib_path)
+    probe.kf_probe_read.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_size_t] + [ctypes.c_void_p] * 2
+    assert probe.kf_probe_read(None, FAKE, 1024, FAKE, None) == 1       # null buffer
+    assert probe.kf_probe_read(FAKE, FAKE, 1000, FAKE, None) == 1       # not a multiple of 16
+    assert probe.kf_probe_read(FAKE + 8, FAKE, 1024, FAKE, None) == 1   # misaligned
+
+
 def test_prefill_threshold():
     assert kf.plan(1, 8, 100, 4, 1, 128).path != "prefill"   # 32 rows per KV head
     assert kf.plan(1, 9, 100, 4, 1, 128).path == "prefill"   # 36 rows

@@ -13,11 +13,12 @@ RATIOS = [1, 2, 4, 8, 16, 32]
 
 @settings(max_examples=400, deadline=None)
 @given(B=st.integers(1, 64), H_kv=st.sampled_from([1, 2, 4, 8]), ratio=st.sampled_from(RATIOS),
-       q=st.integers(1, 300), kv=st.integers(1, 300000), D=st.sampled_from([16, 64, 128, 256]))
-def test_plan_invariants(B, H_kv, ratio, q, kv, D):
+       q=st.integers(1, 300), kv=st.integers(1, 300000), D=st.sampled_from([16, 64, 128, 256]),
+       cus=st.sampled_from([32, 80, 256, 304]))
+def test_plan_invariants(B, H_kv, ratio, q, kv, D, cus):
     H_q = H_kv * ratio
     try:
-        p = kf.plan(B, q, kv, H_q, H_kv, D)
+        p = kf.plan(B, q, kv, H_q, H_kv, D, num_cus=cus)
     except kf.KfError as e:
         # Only shapes beyond 32-bit in-head indexing are refused.
         assert e.status == kf.KF_ERR_SIZE
