@@ -51,7 +51,9 @@ enum kf_status {
     KF_ERR_WORKSPACE = 5,  /* workspace missing or smaller than required        */
     KF_ERR_ALIGN = 6,      /* a device pointer is not 16-byte aligned           */
     KF_ERR_HIP = 7,        /* a HIP runtime call failed: kf_last_hip_error()    */
-    KF_ERR_FLAGS = 8       /* unknown bits in `flags`, or F16 and BF16 together  */
+    KF_ERR_FLAGS = 8,      /* unknown bits in `flags`, or F16 and BF16 together  */
+    KF_ERR_SCRATCH = 9     /* kf_attn_fwd_noalloc: shape needs more scratch than
+                              its static maximum                                 */
 };
 
 /* kf_attn_fwd_ex / kf_attn_decode_paged flags. */
@@ -159,6 +161,28 @@ int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, void* O,
                    int B, int q_len, int kv_len, int H_q, int H_kv, int D,
                    const int* kv_lens, int flags,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* kf_attn_fwd_ex without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference.
+ *
+ * The split-KV partials go to a static device array of the library, one per
+ * device, of kf_attn_noalloc_scratch_bytes() bytes (16 MiB), held until the
+ * process ends; the call makes no hipMalloc / hipFree or any other allocation.
+ * Its address is resolved on the first call on each device (with that device
+ * current on the calling thread).  A shape whose plan needs more than that
+ * (kf_attn_workspace_bytes) returns KF_ERR_SCRATCH and launches nothing.
+ * Every call on one device shares that device's array: calls that can run
+ * concurrently on one device (two streams, two threads) race on it and must
+ * be serialised by the caller; consecutive calls on one stream are safe.  The
+ * kernels need no initialised scratch.  Arguments otherwise as kf_attn_fwd_ex. */
+int kf_attn_fwd_noalloc(const void* Q, const void* K, const void* V, void* O,
+                        float* row_max, float* row_sumexp,
+                        int B, int q_len, int kv_len, int H_q, int H_kv, int D,
+                        const int* kv_lens, int flags, void* stream);
+
+/* Size of kf_attn_fwd_noalloc's static per-device scratch (bytes). */
+size_t kf_attn_noalloc_scratch_bytes(void);
 
 /* Decode over a paged K/V cache, the block-table gather fused into the
  * split-KV decode kernel.  Replaces the gather + attention of the

@@ -35,7 +35,7 @@ __all__ = [
     "KfError", "LIB_PATH", "load_library", "plan", "workspace_bytes", "attn_fwd",
     "attn_fwd_ptr", "launch_flash_attn", "status_string", "exported_symbols",
     "KF_OK", "KF_ERR_HEAD_DIM", "KF_ERR_GQA", "KF_ERR_SIZE", "KF_ERR_NULL",
-    "KF_ERR_WORKSPACE", "KF_ERR_ALIGN", "KF_ERR_HIP", "KF_ERR_FLAGS",
+    "KF_ERR_WORKSPACE", "KF_ERR_ALIGN", "KF_ERR_HIP", "KF_ERR_FLAGS", "KF_ERR_SCRATCH",
     "KF_ATTN_CAUSAL",
     "KF_ATTN_OUT_F16", "KF_ATTN_OUT_BF16", "KF_ATTN_LSE",
     "PATH_NAMES", "attn_fwd_ex_ptr", "attn_decode_paged", "attn_decode_paged_ptr",
@@ -55,6 +55,7 @@ KF_ERR_WORKSPACE = 5
 KF_ERR_ALIGN = 6
 KF_ERR_HIP = 7
 KF_ERR_FLAGS = 8
+KF_ERR_SCRATCH = 9
 KF_ATTN_CAUSAL = 1
 KF_ATTN_OUT_F16 = 2
 KF_ATTN_OUT_BF16 = 4
@@ -142,6 +143,10 @@ def load_library(path: str = LIB_PATH):
     lib.kf_attn_fwd.restype = i
     lib.kf_attn_fwd_ex.argtypes = [p, p, p, p, p, p] + [i] * 6 + [p, i, p, sz, p]
     lib.kf_attn_fwd_ex.restype = i
+    lib.kf_attn_fwd_noalloc.argtypes = [p, p, p, p, p, p] + [i] * 6 + [p, i, p]
+    lib.kf_attn_fwd_noalloc.restype = i
+    lib.kf_attn_noalloc_scratch_bytes.argtypes = []
+    lib.kf_attn_noalloc_scratch_bytes.restype = sz
     lib.kf_attn_decode_paged.argtypes = [p] * 8 + [i] * 9 + [p, sz, p]
     lib.kf_attn_decode_paged.restype = i
     lib.kf_attn_decode_paged_workspace_bytes.argtypes = [i] * 7

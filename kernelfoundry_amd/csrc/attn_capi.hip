@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 #include <climits>
 #include <cstdint>
 #include <cstdio>
@@ -391,6 +392,39 @@ int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const 
     return KF_OK;
 }
 
+// ---- Static split-KV scratch of kf_attn_fwd_noalloc. ----
+// One array per device, resident until the process ends; the entry point
+// uses it in place of a caller workspace and never allocates.  In host code
+// `scratch` names a host-side stand-in, not device memory: only the address
+// hipGetSymbolAddress returns (kept per device) is passed to kernels.
+constexpr size_t kStaticScratchBytes = size_t(16) << 20;
+__device__ __align__(256) char scratch[kStaticScratchBytes];
+
+// Device address of this device's `scratch` (device current on the calling
+// thread), resolved once per device; nullptr and the HIP error on failure.
+void* static_scratch(hipError_t* err) {
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess && (dev < 0 || dev >= kMaxDevices)) e = hipErrorInvalidDevice;
+    if (e != hipSuccess) {
+        *err = e;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+            return nullptr;
+        }
+        addr[dev] = ptr;
+    }
+    return addr[dev];
+}
+
 // Paged geometry: page_size a power of two in [16, 2^20], positive counts,
 // key capacity max_pages_per_seq * page_size within int.  Returns the
 // status and, on success, log2(page_size) and the capacity.
@@ -490,6 +524,27 @@ int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, void* O, float* 
                workspace, workspace_bytes, stream);
 }
 
+int kf_attn_fwd_noalloc(const void* Q, const void* K, const void* V, void* O, float* row_max,
+                        float* row_sumexp, int B, int q_len, int kv_len, int H_q, int H_kv, int D,
+                        const int* kv_lens, int flags, void* stream) {
+    Plan pl;
+    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), &pl);
+    if (st != KF_OK) return st;
+    if (pl.ws_bytes > kStaticScratchBytes) return KF_ERR_SCRATCH;
+    void* ws = nullptr;
+    if (pl.ws_bytes > 0) {
+        hipError_t e = hipSuccess;
+        ws = static_scratch(&e);
+        if (!ws) return hip_fail(e);
+    }
+    kf::AttnParams prm{};
+    prm.kv_lens = kv_lens;
+    return run(pl, prm, Q, K, V, O, row_max, row_sumexp, q_len, kv_len, H_kv, D, flags, ws,
+               pl.ws_bytes, stream);
+}
+
+size_t kf_attn_noalloc_scratch_bytes(void) { return kStaticScratchBytes; }
+
 size_t kf_attn_decode_paged_workspace_bytes(int B, int q_len, int H_q, int H_kv, int D,
                                             int page_size, int max_pages_per_seq) {
     int sh, cap;
@@ -564,6 +619,7 @@ const char* kf_status_string(int status) {
         case KF_ERR_ALIGN: return "device pointer not 16-byte aligned (workspace: 256-byte)";
         case KF_ERR_HIP: return "HIP runtime error (see kf_last_hip_error)";
         case KF_ERR_FLAGS: return "unknown or conflicting flag bits (KF_ATTN_CAUSAL, KF_ATTN_OUT_F16 or KF_ATTN_OUT_BF16, KF_ATTN_LSE)";
+        case KF_ERR_SCRATCH: return "shape needs more split-KV scratch than kf_attn_fwd_noalloc's static maximum (kf_attn_noalloc_scratch_bytes); use kf_attn_fwd_ex with a workspace";
         default: return "unknown status";
     }
 }

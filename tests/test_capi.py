@@ -339,6 +339,28 @@ def test_kernel_names_follow_the_plan(lib):
     assert lib.kf_attn_kernel_names(1, 1, 4096, 32, 8, 100, 0, None, buf, 8) == kf.KF_ERR_HEAD_DIM
 
 
+def test_noalloc_validation(lib):
+    """kf_attn_fwd_noalloc validates like kf_attn_fwd_ex and refuses a shape
+    whose split-KV partials exceed its static scratch before any launch."""
+    assert lib.kf_attn_noalloc_scratch_bytes() == 16 << 20
+    big = (1, 1, 8192, 256, 8, 128)                    # B, q, kv, H_q, H_kv, D: 16.25 MiB
+    assert kf.workspace_bytes(*big) > lib.kf_attn_noalloc_scratch_bytes()
+    B, q, kv, H_q, H_kv, D = big
+    args = (FAKE, FAKE, FAKE, FAKE, None, None)
+    assert lib.kf_attn_fwd_noalloc(*args, B, q, kv, H_q, H_kv, D, None, 0, None) == \
+        kf.KF_ERR_SCRATCH
+    assert lib.kf_attn_fwd_noalloc(*args, 1, 1, 4096, 32, 8, 100, None, 0, None) == \
+        kf.KF_ERR_HEAD_DIM
+    assert lib.kf_attn_fwd_noalloc(*args, 0, 1, 4096, 32, 8, 128, None, 0, None) == kf.KF_ERR_SIZE
+    assert lib.kf_attn_fwd_noalloc(*args, 1, 1, 4096, 30, 8, 128, None, 0, None) == kf.KF_ERR_GQA
+    # A prefill needs no scratch: pointer validation answers first.
+    assert lib.kf_attn_fwd_noalloc(None, FAKE, FAKE, FAKE, None, None, 1, 300, 300, 8, 2, 128,
+                                   None, 0, None) == kf.KF_ERR_NULL
+    assert lib.kf_attn_fwd_noalloc(FAKE, FAKE, FAKE, FAKE, None, None, 1, 300, 300, 8, 2, 128,
+                                   None, 64, None) == kf.KF_ERR_FLAGS
+    assert "static maximum" in kf.status_string(kf.KF_ERR_SCRATCH)
+
+
 def test_probe_library_exports_its_header():
     """libkf_probe.so (bench.py's measurement probes) exports exactly what
     include/kf/probe.h declares."""

@@ -1,0 +1,111 @@
+"""GPU checks of kf_attn_fwd_noalloc, the entry point that allocates nothing
+(its split-KV partials live in the library's static per-device scratch).
+
+Through the C ABI (ctypes), each case runs kf_attn_fwd_ex with a caller
+workspace and kf_attn_fwd_noalloc on the same inputs and compares O, Mi and
+Li bit for bit: both launch the same kernels, so the static scratch must
+change nothing.  Two calls in a row, the second on a smaller input, check
+that the second call is not disturbed by what the first left in the
+scratch.  A shape needing more than the static maximum is refused with
+KF_ERR_SCRATCH and launches nothing.
+"""
+import ctypes
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _announce(**kw):
+    print("case", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    return torch
+
+
+def _inputs(torch, B, H_q, H_kv, q, kv, D, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Q = torch.randn((B, H_q, q, D), generator=g, device="cuda").half()
+    K = torch.randn((B, H_kv, kv, D), generator=g, device="cuda").half()
+    V = torch.randn((B, H_kv, kv, D), generator=g, device="cuda").half()
+    return Q, K, V
+
+
+def _both(torch, kf, B, H_q, H_kv, q, kv, D, seed, flags=0, lens=None):
+    lib = kf.load_library()
+    Q, K, V = _inputs(torch, B, H_q, H_kv, q, kv, D, seed)
+    kvl = None if lens is None else torch.tensor(lens, dtype=torch.int32, device="cuda")
+    kvp = kvl.data_ptr() if kvl is not None else None
+    need = kf.workspace_bytes(B, q, kv, H_q, H_kv, D)
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+    outs = []
+    for noalloc in (False, True):
+        O = torch.full((B, H_q, q, D), float("nan"), device="cuda")
+        Mi = torch.full((B, H_q, q), float("nan"), device="cuda")
+        Li = torch.full((B, H_q, q), float("nan"), device="cuda")
+        s = torch.cuda.current_stream().cuda_stream
+        if noalloc:
+            st = lib.kf_attn_fwd_noalloc(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(),
+                                         Mi.data_ptr(), Li.data_ptr(), B, q, kv, H_q, H_kv, D,
+                                         kvp, flags, s)
+        else:
+            st = lib.kf_attn_fwd_ex(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(),
+                                    Mi.data_ptr(), Li.data_ptr(), B, q, kv, H_q, H_kv, D, kvp,
+                                    flags, ws.data_ptr(), need, s)
+        assert st == kf.KF_OK, kf.status_string(st)
+        outs.append((O, Mi, Li))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    return need
+
+
+@pytest.mark.parametrize("first,second", [
+    # B, H_q, H_kv, q_len, kv_len, D, flags, kv_lens
+    ((1, 32, 8, 1, 4096, 128, 0, None), (1, 32, 8, 1, 1000, 128, 0, None)),
+    ((1, 32, 8, 4, 8192, 128, 1, [8000]), (2, 32, 8, 1, 3000, 128, 1, [3000, 77])),
+    ((1, 32, 1, 1, 2048, 64, 0, None), (1, 16, 1, 1, 700, 64, 0, None)),
+], ids=["c2_then_smaller", "causal_lens_then_smaller", "mqa_then_smaller"])
+def test_noalloc_equals_workspace_entry_on_two_calls(first, second):
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    lib = kf.load_library()
+    scratch = lib.kf_attn_noalloc_scratch_bytes()
+    assert scratch == 16 << 20
+    sizes = []
+    for i, (B, H_q, H_kv, q, kv, D, flags, lens) in enumerate((first, second)):
+        _announce(test="noalloc", call=i, B=B, H_q=H_q, H_kv=H_kv, q=q, kv=kv, D=D, flags=flags,
+                  kv_lens=lens)
+        sizes.append(_both(torch, kf, B, H_q, H_kv, q, kv, D, 100 + i, flags, lens))
+    assert 0 < sizes[1] < sizes[0] <= scratch
+
+
+def test_noalloc_without_scratch_and_after_other_calls():
+    """A prefill (no split-KV scratch) and then a split decode again: the
+    entry point serves both, and the decode result still matches."""
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    _announce(test="noalloc_prefill")
+    assert _both(torch, kf, 1, 8, 2, 300, 300, 128, 7) == 0
+    _announce(test="noalloc_decode_again")
+    assert _both(torch, kf, 1, 32, 8, 1, 4096, 128, 8) > 0
+
+
+def test_noalloc_refuses_a_shape_beyond_its_scratch():
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    lib = kf.load_library()
+    B, H_q, H_kv, q, kv, D = 1, 256, 8, 1, 8192, 128
+    assert kf.workspace_bytes(B, q, kv, H_q, H_kv, D) > lib.kf_attn_noalloc_scratch_bytes()
+    _announce(test="noalloc_oversize")
+    Q, K, V = _inputs(torch, B, H_q, H_kv, q, kv, D, 3)
+    O = torch.full((B, H_q, q, D), 5.0, device="cuda")
+    st = lib.kf_attn_fwd_noalloc(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), None,
+                                 None, B, q, kv, H_q, H_kv, D, None, 0,
+                                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert st == kf.KF_ERR_SCRATCH
+    assert bool((O == 5.0).all())
