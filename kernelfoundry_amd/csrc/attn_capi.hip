@@ -55,7 +55,7 @@ long long decode_stream_splits(long long n_groups, long long max_splits, int D, 
 // are preferred while they still give kShortMinWavesPerCU waves per CU.
 constexpr long long kShortMaxWavesPerCU = 8;
 constexpr long long kShortMinWavesPerCU = 4;
-constexpr int kMinGroupKeys = 128;      // keys before a prefill row's keys are split in two
+constexpr int kMinGroupKeys = 128;      // keys before a prefill row's keys are split between KV groups
 constexpr size_t kWsAlign = 256;
 
 thread_local int g_last_hip_error = 0;
@@ -105,7 +105,7 @@ struct Plan {
     int grid;
     int threads;
     int waves;          // prefill: waves per workgroup
-    int kv_groups;      // prefill: KV groups per workgroup (1 or 2)
+    int kv_groups;      // prefill: KV groups per workgroup (1, 2 or 4)
     int short_stages;   // decode: 32-key stages per split of the short-split kernel, 0 = streaming kernel
     int merge_cw;       // split merge: float4 columns per wave
     int merge_per;      // split merge: splits per lane
@@ -180,16 +180,23 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
         p.path = splits > 1 ? KF_PATH_DECODE_SPLIT : KF_PATH_DECODE;
     } else {
         // Waves per workgroup: the most the head dimension allows.  When that
-        // grid would leave CUs without a workgroup, D = 64 / 128 first split
-        // each row's keys between two KV groups of waves (8 waves x 128 rows,
-        // then 4 waves x 64 rows), which keeps two waves per SIMD; otherwise
-        // the waves are halved (down to 2).  D = 256 stays at 4 waves (its
-        // accumulators need a SIMD per wave).
+        // grid would leave CUs without a workgroup, D = 64 / 128 split each
+        // row's keys between KV groups of waves: two (8 waves x 128 rows),
+        // then four (8 waves x 64 rows) while every group keeps at least
+        // kMinGroupKeys keys, else two groups of 4 waves x 64 rows (two such
+        // workgroups share a CU); all keep two waves per SIMD.  Other head
+        // dimensions halve the waves (down to 2).  D = 256 stays at 4 waves
+        // (its accumulators need a SIMD per wave).
         int nw = kf::prefill_max_waves(D), ks = 1;
         const auto wgs = [&](long long rows) { return n_groups * ((R + rows - 1) / rows); };
         if ((D == 64 || D == 128) && wgs(32 * nw) < cus && kv_len >= kMinGroupKeys) {
             ks = 2;
-            if (wgs(128) < cus) nw = 4;
+            if (wgs(128) < cus) {
+                if (kv_len >= 4LL * kMinGroupKeys)
+                    ks = 4;
+                else
+                    nw = 4;
+            }
         } else {
             const int nw_min = D >= 256 ? 4 : 2;
             while (nw > nw_min && wgs(32 * nw) < cus) nw /= 2;
@@ -240,6 +247,10 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
             launch_prefill<D, 4>(pl, prm, mask, stream);
         } else {
             if constexpr (D == 64 || D == 128) {
+                if (pl.kv_groups == 4) {
+                    launch_prefill<D, 8, 4>(pl, prm, mask, stream);
+                    return hipGetLastError();
+                }
                 if (pl.kv_groups == 2) {
                     if (pl.waves == 8)
                         launch_prefill<D, 8, 2>(pl, prm, mask, stream);

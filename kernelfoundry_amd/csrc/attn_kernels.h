@@ -175,6 +175,18 @@ __device__ __forceinline__ void store_o_row(const AttnParams& p, size_t ri, cons
         }
 }
 
+// store_o_row in p.out_dtype, the format chosen once for the whole row.
+template <int D, int NTD>
+__device__ __forceinline__ void store_o_row_any(const AttnParams& p, size_t ri, const f32x16 (&o)[NTD],
+                                                float inv, int g) {
+    if (p.out_dtype == kOutF16)
+        store_o_row<kOutF16, D>(p, ri, o, inv, g);
+    else if (p.out_dtype == kOutBF16)
+        store_o_row<kOutBF16, D>(p, ri, o, inv, g);
+    else
+        store_o_row<kOutF32, D>(p, ri, o, inv, g);
+}
+
 // Row statistics of query row r: Mi and Li, or LSE = Mi + ln(Li) (-inf for a
 // row without keys) into the Mi slot.
 __device__ __forceinline__ void store_stats(const AttnParams& p, size_t r, float mi, float li) {
@@ -613,9 +625,9 @@ template <> struct SwizzleRow<256> : SwizzleRow<128> {};
 // variant overlaps S(t+1) = K Q^T with the softmax of tile t (a second score
 // block in registers).  D = 256 holds 128 fp32 O accumulators per lane, so it
 // runs 4 waves (one per SIMD, up to 512 registers; it uses ~450).  Grids too
-// small to give every CU a workgroup use fewer rows per workgroup: KS = 2 KV
-// groups (each wave takes half of the keys of its rows, the two halves merged
-// in LDS at the end) and then fewer waves (NW = 4, 2).
+// small to give every CU a workgroup use fewer rows per workgroup: KS = 2 or
+// 4 KV groups (each wave takes 1 / KS of the keys of its rows, the parts
+// merged in LDS at the end) and then fewer waves (NW = 4, 2).
 template <int D> constexpr int kPrefillMaxWaves = D >= 256 ? 4 : 8;
 
 constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
@@ -627,19 +639,28 @@ template <int D, int NW = kPrefillMaxWaves<D>, int KS = 1> struct PrefillCfg {
     static constexpr int kRowWaves = NW / KS;       // waves per KV group
     static constexpr int kThreads = 64 * kWaves;
     static constexpr int kRows = 32 * kRowWaves;    // query rows per workgroup
-    static_assert(NW % KS == 0 && (KS == 1 || D <= 128), "KV groups: D <= 128");
+    static_assert(NW % KS == 0 && (KS == 1 || KS == 2 || KS == 4) && (KS == 1 || D <= 128),
+                  "KV groups: 1, 2 or 4, D <= 128");
     // Register budget: 256 per wave (two waves per SIMD) for D <= 128,
     // whatever the workgroup size, so every variant keeps its accumulators in
     // VGPRs; 512 for D = 256.
     static constexpr int kWavesPerEU = D >= 256 ? 1 : 2;
-    // Stages t, t+1 and the one being filled rotate through three LDS
-    // buffers.  Tiles per LDS stage: 8-wave workgroups without KV groups hold
-    // two tiles per stage, so the workgroup barrier and the LDS-DMA issue come
-    // once per 64 kv rows.  The others keep one tile per stage (48 KB of LDS
-    // per KV group at D = 128, 96 KB in all at D = 256), which holds the
-    // compiler to the 256-register budget at D <= 128.
+    // Tiles per LDS stage: 8-wave workgroups without KV groups hold two tiles
+    // per stage, so the workgroup barrier and the LDS-DMA issue come once per
+    // 64 kv rows.  The others keep one tile per stage, which holds the
+    // compiler to the 256-register budget at D <= 128.  Stages t, t+1 and the
+    // one being filled rotate through three stage buffers per KV group (48 KB
+    // per group at D = 128), except where that does not fit: four KV groups
+    // (192 KB), and two 4-wave groups, whose workgroups should share a CU two
+    // at a time.  Those use two buffers per KV group whose K and V halves are
+    // refilled separately: tile t reads K(t+1) from one buffer and V(t) from
+    // the other, while K(t+2) lands in the first buffer's K half and V(t+1)
+    // in the second's V half (32 KB per group at D = 128).  V then has one
+    // tile of lead instead of two, which measured 2 % (two 8-wave groups) to
+    // 6 % (D = 256) slower where the three buffers fit.
     static constexpr int kSub = (kWaves >= 8 && KS == 1) ? 2 : 1;
     static constexpr int kStageRows = BC * kSub;
+    static constexpr int kBuffers = (KS == 4 || (KS == 2 && NW == 4)) ? 2 : 3;
 };
 
 inline int prefill_max_waves(int D) { return D >= 256 ? kPrefillMaxWaves<256> : kPrefillMaxWaves<128>; }
@@ -762,7 +783,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     constexpr int kNTD = (D < 32 ? 32 : D) / 32;  // 32-row O^T tiles
     __shared__ __attribute__((aligned(1024))) char buf0[KS * S::kStageBytes];
     __shared__ __attribute__((aligned(1024))) char buf1[KS * S::kStageBytes];
-    __shared__ __attribute__((aligned(1024))) char buf2[KS * S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char buf2[Cfg::kBuffers == 3 ? KS * S::kStageBytes : 16];
     __shared__ __attribute__((aligned(16))) char zero_pad[16];  // D=16: V^T rows 16..31
 
     const int tid = threadIdx.x;
@@ -824,7 +845,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     if constexpr (KS > 1) wave_min = min(wave_min, kv_end) - kv_base;
     char* const b0 = buf0 + kgrp * S::kStageBytes;  // this group's stage regions
     char* const b1 = buf1 + kgrp * S::kStageBytes;
-    char* const b2 = buf2 + kgrp * S::kStageBytes;
+    char* const b2 = Cfg::kBuffers == 3 ? buf2 + kgrp * S::kStageBytes : buf2;  // unused at 2
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
     const char* Kh = reinterpret_cast<const char*>(p.K + (size_t)grp * kv_len * D);
@@ -850,10 +871,13 @@ void kf_attn_prefill_kernel(AttnParams p) {
         lane_base[i] = (uint32_t)(lr * S::kRowBytes +
                                   (((lane % S::kChunks) ^ SW::h(r)) % S::kChunks) * 16);
     }
-    // kv0: first key of the stage relative to this group's kv_base.
-    auto issue_stage = [&](char* dst, int kv0_rel) {
-        const int kv0 = kv_base + kv0_rel;
-        if (kv0 + SR <= kv_len) {
+    // Copy K rows [kv0k, kv0k + SR) into the K half of kdst (when do_k) and
+    // V rows [kv0v, kv0v + SR) into the V half of vdst (when do_v); kv0k /
+    // kv0v relative to this group's kv_base, kv0k >= kv0v when both are
+    // copied.  The flags are wave-uniform.
+    auto issue = [&](char* kdst, int kv0k_rel, bool do_k, char* vdst, int kv0v_rel, bool do_v) {
+        const int kv0k = kv_base + kv0k_rel, kv0v = kv_base + kv0v_rel;
+        if ((do_k ? kv0k : kv0v) + SR <= kv_len) {
             // Full stage: wave-uniform row base (SGPRs) + the lane's constant
             // 32-bit offset; no per-lane address arithmetic.
 #pragma unroll
@@ -861,10 +885,12 @@ void kf_attn_prefill_kernel(AttnParams p) {
                 const int j = wave + kRowWaves * i;
                 if (S::kInstrTotal % kRowWaves == 0 || j < S::kInstrTotal) {
                     const bool is_v = j >= S::kInstrPerTensor;
+                    if (!(is_v ? do_v : do_k)) continue;
                     const int ii = j % S::kInstrPerTensor;
+                    const int kv0 = is_v ? kv0v : kv0k;
                     const char* base = (is_v ? Vh : Kh) +
                                        (size_t)(kv0 + ii * S::kRowsPerInstr) * S::kRowBytes;
-                    char* d = dst + (is_v ? S::kTensorBytes : 0) + ii * 1024;
+                    char* d = (is_v ? vdst + S::kTensorBytes : kdst) + ii * 1024;
                     // Keep the 32-bit lane offset opaque so the address stays
                     // "SGPR base + VGPR offset" instead of a hoisted 64-bit sum.
                     uint32_t lb = lane_base[i % kLBPeriod];
@@ -882,16 +908,18 @@ void kf_attn_prefill_kernel(AttnParams p) {
                 const int j = wave + kRowWaves * i;
                 if (S::kInstrTotal % kRowWaves == 0 || j < S::kInstrTotal) {
                     const bool is_v = j >= S::kInstrPerTensor;
+                    if (!(is_v ? do_v : do_k)) continue;
                     const int ii = j % S::kInstrPerTensor;
-                    const int kv = min(kv0 + ii * S::kRowsPerInstr + lr, kv_len - 1);
+                    const int kv = min((is_v ? kv0v : kv0k) + ii * S::kRowsPerInstr + lr, kv_len - 1);
                     const uint32_t off = (uint32_t)kv * S::kRowBytes +
                                          (lane_base[i % kLBPeriod] - (uint32_t)(lr * S::kRowBytes));
-                    char* d = dst + (is_v ? S::kTensorBytes : 0) + ii * 1024;
+                    char* d = (is_v ? vdst + S::kTensorBytes : kdst) + ii * 1024;
                     __builtin_amdgcn_global_load_lds((is_v ? Vh : Kh) + off, (lds_void*)d, 16, 0, 0);
                 }
             }
         }
     };
+    auto issue_stage = [&](char* dst, int kv0_rel) { issue(dst, kv0_rel, true, dst, kv0_rel, true); };
 
     // ---- Per-lane LDS read offsets (bytes within a stage). ----
     // K (A of S^T = K Q^T): row l%32, logical chunk 2 kk + g.
@@ -989,9 +1017,10 @@ void kf_attn_prefill_kernel(AttnParams p) {
     if constexpr (kMask) lim_lane = row < R ? row_kv_limit(p, kvb, row % p.q_len) : blk_lim;
     if constexpr (KS > 1) lim_lane = min(lim_lane, kv_end) - kv_base;
 
-    // ---- Prologue: stage 0 (and 1 when pipelined) in flight, Q fragments, S(0). ----
+    // ---- Prologue: stage 0 and the K of stage 1 (two-buffer ring) or all of
+    // stage 1 (three buffers) in flight, Q fragments, S(0). ----
     issue_stage(b0, 0);
-    if (nstages > 1) issue_stage(b1, SR);
+    if (nstages > 1) issue(b1, SR, true, b1, SR, Cfg::kBuffers == 3);
     f16x8 qf[kNKK];
     load_q_frags<D>(Qg, row, R, lane, qf);
     if constexpr (D < 32) {
@@ -1014,24 +1043,32 @@ void kf_attn_prefill_kernel(AttnParams p) {
     auto neg_m = [&]() { return ((kMask || KS > 1) && st.m == -INFINITY) ? 0.f : -st.m; };
 
     // ---- One pipelined tile; S(t) and its running max are ready on entry.
-    //   barrier; LDS-DMA of stage t+2
+    //   barrier; LDS-DMA of the next stage(s)
     //   S(t+1) = K(t+1) Q^T   | exp + fp16 pack of S(t)
     //   O += V(t) P(t)        | row max of S(t+1)
     //   rare: tail masking of S(t+1); lazy rescale of O
-    // Stages rotate through three LDS buffers.  On the last tile the S(t+1)
-    // MFMAs read a stale, in-bounds buffer and are discarded, which keeps the
+    // cur holds V(t), nxt holds K(t+1).  On the last tile the S(t+1) MFMAs
+    // read a stale, in-bounds buffer and are discarded, which keeps the
     // overlapped regions free of branches (issue is in order: a wave can only
     // overlap MFMA and VALU work that is interleaved in its own stream).
-    auto tile = [&](const char* cur, const char* nxt, char* fill, int t, bool sync) {
+    auto tile = [&](char* cur, char* nxt, char* fill, int t, bool sync) {
         f16x8 pp[2 * kNSB];
         if (sync) {
-            // Tile t is the last of its stage j = t / kSub, tile t+1 the first
-            // of stage j+1: wait until stage j+1 landed for every wave; stage
-            // j-1 (last read by tile t-1) is then free for stage j+2.
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
-            const int js = t / kSub + 2;
-            if (js < nstages) issue_stage(fill, js * SR);
+            if constexpr (Cfg::kBuffers == 2) {
+                // One tile per stage, two buffers: K(t+1) and V(t) landed for
+                // every wave; tile t-1 read K(t) from cur and V(t-1) from nxt,
+                // so K(t+2) goes to cur's K half and V(t+1) to nxt's V half.
+                const bool dk = t + 2 < nstages, dv = t + 1 < nstages;
+                if (dk || dv) issue(cur, (t + 2) * SR, dk, nxt, (t + 1) * SR, dv);
+            } else {
+                // Three buffers: tile t is the last of its stage j = t / kSub,
+                // tile t+1 the first of stage j+1, which has landed for every
+                // wave; stage j-1 (last read by tile t-1) is free for j+2.
+                const int js = t / kSub + 2;
+                if (js < nstages) issue_stage(fill, js * SR);
+            }
         }
         f32x16 sn[kNSB];
         qk(nxt, qf, sn);
@@ -1051,7 +1088,15 @@ void kf_attn_prefill_kernel(AttnParams p) {
             for (int b = 0; b < kNSB; ++b) sc[b] = sn[b];
         }
     };
-    if constexpr (kSub == 1) {
+    if constexpr (kSub == 1 && Cfg::kBuffers == 2) {
+        // Tile t reads V(t) from buffer t % 2 and K(t+1) from buffer (t+1) % 2.
+        for (int t = 0; t < ntiles; t += 2) {
+            tile(b0, b1, nullptr, t, true);
+            if (t + 1 >= ntiles) break;
+            tile(b1, b0, nullptr, t + 1, true);
+        }
+    } else if constexpr (kSub == 1) {
+        // Stage t lives in buffer t % 3.
         for (int t = 0; t < ntiles; t += 3) {
             tile(b0, b1, b2, t, true);
             if (t + 1 >= ntiles) break;
@@ -1080,72 +1125,82 @@ void kf_attn_prefill_kernel(AttnParams p) {
     }
 
     if constexpr (KS > 1) {
-        // ---- KV-group merge.  Each group rebases its state to its true row
-        // max: O_g, m_g = rmax scale (natural log), l_g (both half rows);
-        // a group that saw no key of a row has weight 0.  Groups 1 .. KS-1
-        // publish O_g in lane-private slots of the (now free) stage buffers
-        // and (m_g, l_g) in merge_ml; group 0 combines
-        //   O = sum_g w_g O_g / L, L = sum_g w_g l_g, w_g = exp(m_g - max_g m_g).
-        constexpr int kSlotFloats = kNTD * 16 * 64;      // one wave's O
-        constexpr int kSlots = (KS - 1) * kRowWaves;
-        static_assert(kSlotFloats * 4 <= S::kStageBytes && kSlots <= 3 * KS, "merge slots");
-        __shared__ float merge_ml[2 * kSlots * 64];
+        // ---- KV-group merge, spread over the groups.  Each group rebases its
+        // state to its true row max: O_g beta_g, m_g = rmax scale (natural
+        // log), l_g beta_g (both half rows); a group that saw no key of a row
+        // has weight 0.  A lane's O is kC float4 chunks (chunk cc holds
+        // d = 32 (cc / 4) + 8 (cc % 4) + 4 (l / 32) .. +3); group h owns
+        // chunks [h kCPer, (h+1) kCPer).  Every group publishes (m_g, l_g)
+        // and the chunks it does not own in lane-private 1 KiB slots of the
+        // (now free) stage buffers; after one barrier every group merges and
+        // stores its own chunks,
+        //   O = sum_g w_g O_g / L,  L = sum_g w_g l_g,  w_g = exp(m_g - max m),
+        // summing over g = 0 .. KS-1 in that order whatever the owner, so the
+        // result does not depend on which group stores a chunk.
+        constexpr int kC = kNTD * 4;                        // float4 chunks per lane
+        constexpr int kCPer = kC / KS;                      // chunks each group stores
+        constexpr int kSlotsPerBuf = KS * S::kStageBytes / 1024;
+        static_assert(kC % KS == 0, "chunks per group");
+        static_assert(kRowWaves * kC * (KS - 1) <= Cfg::kBuffers * kSlotsPerBuf, "merge slots");
+        __shared__ float merge_ml[2 * KS * kRowWaves * 64];
+        // Slot of chunk cc of row wave w written by group gw (!= owner h).
+        auto slot = [&](int cc, int gw, int h) {
+            const int k = (wave * kC + cc) * (KS - 1) + (gw < h ? gw : gw - 1);
+            char* bb = k / kSlotsPerBuf == 0 ? buf0 : (k / kSlotsPerBuf == 1 ? buf1 : buf2);
+            return reinterpret_cast<f32x4*>(bb + (k % kSlotsPerBuf) * 1024) + lane;
+        };
+        auto chunk = [&](int cc) {
+            const int td = cc / 4, i = cc % 4;
+            return f32x4{o[td][4 * i], o[td][4 * i + 1], o[td][4 * i + 2], o[td][4 * i + 3]};
+        };
         const float l_pair = sum_xor32(st.l);
         const bool none = st.rmax == -INFINITY;
         const float m_g = none ? -INFINITY : st.rmax * p.scale;
         const float beta = none ? 0.f : exp2_hw(st.m - st.rmax * p.scale_log2);
-        auto slot = [&](int sidx) {
-            char* bb = sidx / KS == 0 ? buf0 : (sidx / KS == 1 ? buf1 : buf2);
-            return reinterpret_cast<float*>(bb + (sidx % KS) * S::kStageBytes);
-        };
         __syncthreads();  // every group is done with its stage regions
-        if (kgrp > 0) {
-            const int sidx = (kgrp - 1) * kRowWaves + wave;
-            float* so = slot(sidx);
+        merge_ml[(kgrp * kRowWaves + wave) * 64 + lane] = m_g;
+        merge_ml[((KS + kgrp) * kRowWaves + wave) * 64 + lane] = l_pair * beta;
 #pragma unroll
-            for (int td = 0; td < kNTD; ++td)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) so[(td * 16 + r) * 64 + lane] = o[td][r] * beta;
-            merge_ml[sidx * 64 + lane] = m_g;
-            merge_ml[(kSlots + sidx) * 64 + lane] = l_pair * beta;
+        for (int cc = 0; cc < kC; ++cc) {
+            const int h = cc / kCPer;
+            if (h != kgrp) *slot(cc, kgrp, h) = chunk(cc) * beta;
         }
         __syncthreads();
-        if (kgrp > 0) return;
-        float m_all = m_g;
+        float m_all = -INFINITY;
 #pragma unroll
-        for (int gg = 1; gg < KS; ++gg) m_all = fmaxf(m_all, merge_ml[((gg - 1) * kRowWaves + wave) * 64 + lane]);
-        const float w0 = none ? 0.f : exp2_hw((m_g - m_all) * kLog2e) * beta;
-        float L = w0 * l_pair;
+        for (int gg = 0; gg < KS; ++gg) m_all = fmaxf(m_all, merge_ml[(gg * kRowWaves + wave) * 64 + lane]);
+        float wgt[KS];
+        float L = 0.f;
 #pragma unroll
-        for (int td = 0; td < kNTD; ++td) o[td] *= w0;
-#pragma unroll
-        for (int gg = 1; gg < KS; ++gg) {
-            const int sidx = (gg - 1) * kRowWaves + wave;
-            const float mo = merge_ml[sidx * 64 + lane];
-            const float wg = mo == -INFINITY ? 0.f : exp2_hw((mo - m_all) * kLog2e);
-            L += wg * merge_ml[(kSlots + sidx) * 64 + lane];
-            const float* so = slot(sidx);
-#pragma unroll
-            for (int td = 0; td < kNTD; ++td)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[td][r] += wg * so[(td * 16 + r) * 64 + lane];
+        for (int gg = 0; gg < KS; ++gg) {
+            const float mo = merge_ml[(gg * kRowWaves + wave) * 64 + lane];
+            wgt[gg] = mo == -INFINITY ? 0.f : exp2_hw((mo - m_all) * kLog2e);
+            L += wgt[gg] * merge_ml[((KS + gg) * kRowWaves + wave) * 64 + lane];
         }
-        if (row < R) {
-            const float inv = L > 0.f ? 1.0f / L : 0.f;
-            const size_t ri = (size_t)grp * R + row;
+        const float inv = L > 0.f ? 1.0f / L : 0.f;
+        const size_t ri = (size_t)grp * R + row;
+        auto merge_store = [&](auto out) {
+            constexpr int kOut = decltype(out)::value;
 #pragma unroll
-            for (int td = 0; td < kNTD; ++td)
+            for (int cc = 0; cc < kC; ++cc) {
+                if (cc / kCPer != kgrp) continue;
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int d = 32 * td + 8 * i + 4 * g;
-                    if (d < D) {
-                        f32x4 v = {o[td][4 * i] * inv, o[td][4 * i + 1] * inv,
-                                   o[td][4 * i + 2] * inv, o[td][4 * i + 3] * inv};
-                        store_out4(p, ri * D + d, v);
-                    }
+                for (int gg = 0; gg < KS; ++gg) {
+                    const f32x4 v = gg == kgrp ? chunk(cc) * beta : *slot(cc, gg, kgrp);
+                    acc = wgt[gg] * v + acc;
                 }
-            if (g == 0) store_stats(p, ri, m_all, L);
-        }
+                const int d = 32 * (cc / 4) + 8 * (cc % 4) + 4 * g;
+                if (row < R && d < D) store_out4_as<kOut>(p, ri * D + d, acc * inv);
+            }
+        };
+        if (p.out_dtype == kOutF16)
+            merge_store(std::integral_constant<int, kOutF16>{});
+        else if (p.out_dtype == kOutBF16)
+            merge_store(std::integral_constant<int, kOutBF16>{});
+        else
+            merge_store(std::integral_constant<int, kOutF32>{});
+        if (kgrp == 0 && row < R && g == 0) store_stats(p, ri, m_all, L);
         return;
     }
 
@@ -1155,17 +1210,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
     if (row < R) {
         const float inv = empty ? 0.f : 1.0f / l;
         const size_t ri = (size_t)grp * R + row;
-#pragma unroll
-        for (int td = 0; td < kNTD; ++td)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int d = 32 * td + 8 * i + 4 * g;
-                if (d < D) {
-                    f32x4 v = {o[td][4 * i] * inv, o[td][4 * i + 1] * inv,
-                               o[td][4 * i + 2] * inv, o[td][4 * i + 3] * inv};
-                    store_out4(p, ri * D + d, v);
-                }
-            }
+        store_o_row_any<D>(p, ri, o, inv, g);
         if (g == 0)
             store_stats(p, ri, st.rmax * p.scale,
                         empty ? 0.f : l * exp2_hw(st.m - st.rmax * p.scale_log2));
@@ -1616,12 +1661,7 @@ void kf_attn_decode_short_kernel(AttnParams p) {
             }
         } else {
             const float inv = empty ? 0.f : 1.0f / l;
-            if (p.out_dtype == kOutF16)
-                store_o_row<kOutF16, D>(p, ri, o, inv, g);
-            else if (p.out_dtype == kOutBF16)
-                store_o_row<kOutBF16, D>(p, ri, o, inv, g);
-            else
-                store_o_row<kOutF32, D>(p, ri, o, inv, g);
+            store_o_row_any<D>(p, ri, o, inv, g);
             if (g == 0) store_stats(p, ri, m_nat, empty ? 0.f : l);
         }
     }

@@ -171,8 +171,9 @@ def test_plans_for_baseline_configs():
     assert p.path == "prefill" and p.rows_per_group == 4 * 4096
     assert p.grid_blocks == 8 * (4 * 4096 // rows_per_block)
     p = kf.plan(1, 512, 512, 32, 8, 128)             # C1: 64 8-wave blocks would idle CUs
-    assert p.path == "prefill" and p.block_threads == 256  # 2 row waves x 2 KV groups
+    assert p.path == "prefill" and p.block_threads == 512  # 2 row waves x 4 KV groups
     assert p.grid_blocks == 8 * (4 * 512 // 64) == 256
+    assert kf.kernel_names(1, 512, 512, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 4>"
     assert p.workspace_bytes == 0
     assert p.splits_per_block == 0
     p = kf.plan(1, 1, 4096, 32, 8, 128)              # C2 decode: 1024 one-wave splits
@@ -241,29 +242,35 @@ def test_decode_split_counts(B, H_kv, kv, D, splits, per_block):
     assert p.num_splits * p.kv_per_split >= kv
 
 
-@pytest.mark.parametrize("S,H_kv,D,waves,rows", [
-    (4096, 8, 128, 8, 256), (2048, 8, 128, 8, 256), (1024, 8, 128, 8, 128), (512, 8, 128, 4, 64),
-    (256, 8, 128, 4, 64), (100, 8, 128, 2, 64), (2048, 1, 64, 8, 256), (512, 1, 64, 4, 64), (1024, 1, 64, 8, 128),
-    (130, 2, 256, 4, 128), (4096, 8, 256, 4, 128),
+@pytest.mark.parametrize("S,H_kv,D,waves,groups", [
+    (4096, 8, 128, 8, 1), (2048, 8, 128, 8, 1), (1024, 8, 128, 8, 2), (512, 8, 128, 8, 4),
+    (256, 8, 128, 4, 2), (100, 8, 128, 2, 1), (2048, 1, 64, 8, 1), (512, 1, 64, 8, 4), (1024, 1, 64, 8, 2),
+    (130, 2, 256, 4, 1), (4096, 8, 256, 4, 1),
 ])
-def test_prefill_waves_per_workgroup(S, H_kv, D, waves, rows):
-    """Waves and query rows per workgroup: 8 waves x 256 rows (4 x 128 at
-    D = 256) when that grid gives every CU a workgroup.  Otherwise D = 64 / 128
-    split each row's keys between two KV groups of waves (8 waves x 128 rows,
-    then 4 x 64) if there are at least 128 keys, and the remaining cases
-    halve the waves (down to 2, or 4 at D = 256)."""
+def test_prefill_waves_per_workgroup(S, H_kv, D, waves, groups):
+    """Waves and KV groups per workgroup (32 query rows per wave of a KV
+    group): 8 waves x 256 rows (4 x 128 at D = 256) when that grid gives every
+    CU a workgroup.  Otherwise D = 64 / 128 split each row's keys between KV
+    groups of waves if there are at least 128 keys: two (8 waves x 128 rows),
+    then four (8 waves x 64 rows) if every group keeps 128 keys, else two of
+    4 waves x 64 rows; the remaining cases halve the waves (down to 2, or 4 at
+    D = 256)."""
     p = kf.plan(1, S, S, 32, H_kv, D)
     assert p.path == "prefill" and p.block_threads == 64 * waves
+    assert kf.kernel_names(1, S, S, 32, H_kv, D) == \
+        f"kf_attn_prefill_kernel<{D}, false, {waves}, {groups}>"
+    rows = 32 * waves // groups
     R = 32 // H_kv * S
     assert p.grid_blocks == H_kv * -(-R // rows)
     full = H_kv * -(-R // (256 if D <= 128 else 128)) >= 256
     if full:
-        assert rows == (256 if D <= 128 else 128)
+        assert rows == (256 if D <= 128 else 128) and groups == 1
     elif D <= 128 and S >= 128:
-        assert rows == 32 * waves // 2                      # two KV groups
+        assert groups in (2, 4) and waves >= 4
         assert rows == 64 or H_kv * -(-R // 128) >= 256
+        assert groups < 4 or S >= 4 * 128
     else:
-        assert rows == 32 * waves
+        assert groups == 1
 
 
 @pytest.mark.parametrize("cus", [32, 80, 256])
@@ -280,7 +287,7 @@ def test_plans_scale_with_the_device_cu_count(cus):
     elif 8 * (4 * 512 // 128) >= cus:
         assert p.block_threads == 512 and p.grid_blocks == 128         # 2 KV groups, 128 rows
     else:
-        assert p.block_threads == 256 and p.grid_blocks == 256         # 2 KV groups, 64 rows
+        assert p.block_threads == 512 and p.grid_blocks == 256         # 4 KV groups, 64 rows
     # C3 prefill: 512 workgroups whatever the device.
     assert kf.plan(1, 4096, 4096, 32, 8, 128, num_cus=cus).grid_blocks == 512
     # C2 decode: short splits while 1024 one-wave splits fit 8 per CU.
@@ -328,7 +335,8 @@ def test_kernel_names_follow_the_plan(lib):
         "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, masked=True) == \
         "kf_attn_prefill_kernel<128, true, 8, 1>"
-    assert kf.kernel_names(1, 512, 512, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 4, 2>"
+    assert kf.kernel_names(1, 512, 512, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 4>"
+    assert kf.kernel_names(1, 256, 256, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 4, 2>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_kernel<256, false, 4, 1>"
     assert kf.kernel_names(1, 1, 4096, 32, 8, 128) == \
         "kf_attn_decode_short_kernel<128, 1> + kf_attn_split_merge_kernel<128, 8, 4>"

@@ -31,11 +31,12 @@ def test_plan_invariants(B, H_kv, ratio, q, kv, D, cus):
         assert R > 32
         waves = p.block_threads // 64
         assert waves in ((4,) if D == 256 else (2, 4, 8))
-        # A workgroup holds 32 query rows per wave, or 16 when its waves form
-        # two KV groups (each taking half of the keys); row tiles cover R.
+        # A workgroup holds 32 query rows per wave, or 32 per wave of one of
+        # its two or four KV groups (each taking that share of the keys); row
+        # tiles cover R.
         assert p.grid_blocks % n_groups == 0
         tiles = p.grid_blocks // n_groups
-        assert tiles in (-(-R // (32 * waves)), -(-R // (16 * waves)))
+        assert tiles in (-(-R // (32 * waves)), -(-R // (16 * waves)), -(-R // (8 * waves)))
         assert p.workspace_bytes == 0 and p.num_splits == 1
         return
     assert R <= 32

@@ -104,18 +104,24 @@ def test_prefill_8wave_masked_matches_unmasked_bitwise():
 
 # ---------------------------------------------------------------------------
 # KV groups: grids too small for 8-wave workgroups split each row's keys
-# between two groups of waves (8 waves x 128 rows, or 4 x 64), merged in LDS.
+# between two groups of waves (8 waves x 128 rows, or 4 x 64) or four (8 waves
+# x 64 rows, at least 512 keys), merged in LDS.
 # ---------------------------------------------------------------------------
 KV_GROUP_CASES = [
     # B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens, threads, rows   what it hits
     (1, 32, 8, 1024, 1024, 128, False, None, 512, 128),        # sweep S=1024: 8 waves x 2 groups
-    (1, 32, 8, 512, 512, 128, False, None, 256, 64),           # C1 shape: 4 waves x 2 groups
-    (1, 32, 8, 512, 130, 128, False, None, 256, 64),           # 5 tiles: groups of 3 and 2 (+ tail)
+    (1, 32, 8, 512, 512, 128, False, None, 512, 64),           # C1 shape: 8 waves x 4 groups
+    (1, 32, 8, 512, 520, 128, False, None, 512, 64),           # 4 groups, ragged last group
+    (1, 32, 8, 512, 600, 128, True, None, 512, 64),            # 4 groups, causal, q_len < kv_len
+    (1, 32, 8, 512, 512, 128, False, [100], 512, 64),          # 4 groups of one tile each
+    (1, 32, 8, 512, 512, 128, True, [20], 512, 64),            # groups 1..3 see no key
+    (1, 32, 8, 512, 130, 128, False, None, 256, 64),           # 4 waves x 2 groups: 3 and 2 tiles
     (1, 32, 8, 512, 128, 128, False, None, 256, 64),           # exactly 4 tiles
     (2, 32, 8, 256, 300, 128, True, [300, 129], 256, 64),      # causal + key counts
     (2, 32, 8, 256, 256, 128, True, [256, 40], 256, 64),       # second group sees no key
     (1, 32, 1, 1024, 1024, 64, False, None, 512, 128),         # MQA D=64, 8 waves x 2 groups
-    (1, 32, 1, 512, 700, 64, True, None, 256, 64),             # MQA D=64 causal, q_len < kv_len
+    (1, 32, 1, 512, 512, 64, False, None, 512, 64),            # MQA D=64, 8 waves x 4 groups
+    (1, 32, 1, 512, 700, 64, True, None, 512, 64),             # MQA D=64 causal, 4 groups
 ]
 
 
@@ -127,7 +133,7 @@ def test_kv_groups_parity(case):
     pl = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
     R = H_q // H_kv * q_len
     assert pl.path == "prefill" and pl.block_threads == threads, pl
-    assert pl.grid_blocks == B * H_kv * -(-R // rows), pl       # two KV groups per workgroup
+    assert pl.grid_blocks == B * H_kv * -(-R // rows), pl       # KV groups per workgroup
     _announce(test="kv_groups", B=B, H_kv=H_kv, q_len=q_len, kv_len=kv_len, D=D, causal=causal,
               kv_lens=kv_lens, grid=pl.grid_blocks)
     q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, q_len, kv_len, D, 47000 + kv_len + D)

@@ -4,8 +4,8 @@ Shapes, masks and output formats are drawn from a fixed seed so that, taken
 together, they cross every dispatch the planner makes: the short-split decode
 kernel (32- and 64-key splits) and the streaming decode kernel, each with and
 without the split merge, and the prefill kernel in every workgroup layout
-(8 waves x 256 rows, two KV groups of 8 or 4 waves, 4 and 2 waves; D = 256
-with 4 waves), with causal masking, per-sequence key counts (empty sequences
+(8 waves x 256 rows, two KV groups of 8 or 4 waves, four KV groups of 8
+waves, 4 and 2 waves; D = 256 with 4 waves), with causal masking, per-sequence key counts (empty sequences
 included), ragged lengths and every head dimension.  Each case is
 compared with oracle/attn_oracle.py's fp64 ``sdpa`` on the same fp16 inputs at
 the north-star bar (max |got - ref| <= 2e-3, ||got - ref|| / ||ref|| <= 1e-2;
@@ -56,6 +56,10 @@ def _cases(n=40, seed=2026):
     out.append((32, 8, 8, 1, 200, 16, True, [int(x) for x in rng.integers(0, 201, size=32)], 16))
     out.append((1, 4, 2, 1, 8192, 128, False, None, 17))
     out.append((1, 4, 2, 1, 300, 256, True, [257], 18))
+    # Four KV groups (grid of < 256 workgroups x 128 rows, >= 512 keys): a
+    # ragged last group, and key counts that leave groups without keys.
+    out.append((1, 16, 4, 300, 900, 128, False, None, 19))
+    out.append((2, 16, 2, 200, 1100, 64, True, [1100, 70], 20))
     return out
 
 
@@ -65,14 +69,13 @@ CASES = _cases()
 def _layout(kf, B, H_q, H_kv, q_len, kv_len, D):
     """(path, kernel) for decode, kernel "short32" / "short64" (one wave per
     split of that many keys) or "stream"; ("prefill", waves, kv_groups) for
-    prefill, where kv_groups follows from the grid: two KV groups put
-    16 * waves query rows in a workgroup, one group 32 * waves."""
+    prefill, read from the kernel name (kf_attn_prefill_kernel<D, mask,
+    waves, kv_groups>)."""
     p = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
     if p.path != "prefill":
         return (p.path, f"short{p.kv_per_split}" if p.splits_per_block == 4 else "stream")
-    waves = p.block_threads // 64
-    R = H_q // H_kv * q_len
-    groups = 2 if p.grid_blocks == B * H_kv * -(-R // (16 * waves)) and waves >= 4 and D <= 128 else 1
+    name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D)
+    waves, groups = (int(x) for x in name.rstrip(">").split(",")[-2:])
     return ("prefill", waves, groups)
 
 
@@ -82,7 +85,7 @@ def test_sweep_covers_every_dispatch():
     seen = {_layout(kf, *c[:6]) for c in CASES}
     want = {("decode", "short32"), ("decode_split", "short32"), ("decode_split", "short64"),
             ("decode", "stream"), ("decode_split", "stream"),
-            ("prefill", 8, 1), ("prefill", 8, 2), ("prefill", 4, 2), ("prefill", 4, 1),
+            ("prefill", 8, 1), ("prefill", 8, 2), ("prefill", 8, 4), ("prefill", 4, 2), ("prefill", 4, 1),
             ("prefill", 2, 1)}
     assert want <= seen, sorted(seen)
     # The split merge at its widest: 256 partials per row (4 columns per wave).
