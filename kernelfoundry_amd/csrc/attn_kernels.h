@@ -785,6 +785,10 @@ void kf_attn_prefill_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(1024))) char buf1[KS * S::kStageBytes];
     __shared__ __attribute__((aligned(1024))) char buf2[Cfg::kBuffers == 3 ? KS * S::kStageBytes : 16];
     __shared__ __attribute__((aligned(16))) char zero_pad[16];  // D=16: V^T rows 16..31
+    // 8-wave workgroups with KV groups: the workgroup's query rows, copied
+    // once into LDS (K's row layout) instead of KS times from memory.
+    constexpr bool kQLds = KS > 1 && NW == 8;
+    __shared__ __attribute__((aligned(1024))) char q_lds[kQLds ? Cfg::kRows * D * 2 : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1022,12 +1026,38 @@ void kf_attn_prefill_kernel(AttnParams p) {
     issue_stage(b0, 0);
     if (nstages > 1) issue(b1, SR, true, b1, SR, Cfg::kBuffers == 3);
     f16x8 qf[kNKK];
-    load_q_frags<D>(Qg, row, R, lane, qf);
+    if constexpr (kQLds) {
+        // LDS-DMA of rows [rt kPrefillRows, + kPrefillRows) of the group (rows
+        // past R re-read row R - 1, as load_q_frags does); lane l of KiB j
+        // fills row 4 j + l / kChunks (D = 128) at physical chunk l % kChunks.
+        constexpr int kQInstr = kPrefillRows * S::kRowBytes / 1024;
+        const char* Qb = reinterpret_cast<const char*>(Qg);
+        const int lr = lane / S::kChunks;
+#pragma unroll
+        for (int j0 = 0; j0 < kQInstr; j0 += NW) {
+            const int j = j0 + wave_id;
+            if (kQInstr % NW == 0 || j < kQInstr) {
+                const int r = j * S::kRowsPerInstr + lr;
+                const int src = min(rt * kPrefillRows + r, R - 1);
+                const uint32_t off = (uint32_t)src * S::kRowBytes +
+                                     (uint32_t)((((lane % S::kChunks) ^ SW::h(r)) % S::kChunks) * 16);
+                __builtin_amdgcn_global_load_lds(Qb + off, (lds_void*)(q_lds + j * 1024), 16, 0, 0);
+            }
+        }
+    } else {
+        load_q_frags<D>(Qg, row, R, lane, qf);
+    }
     if constexpr (D < 32) {
         if (tid < 4) reinterpret_cast<uint32_t*>(zero_pad)[tid] = 0u;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if constexpr (kQLds) {
+        // Row wave w's 32 rows start at LDS row 32 w; koff addresses row l % 32.
+#pragma unroll
+        for (int kk = 0; kk < kNKK; ++kk)
+            qf[kk] = *reinterpret_cast<const f16x8*>(q_lds + wave * 32 * S::kRowBytes + koff[kk]);
+    }
 
     RowState st{-INFINITY, -INFINITY, 0.f, -INFINITY};
     const float inv_c = 1.0f / c;
