@@ -793,7 +793,11 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wave = KS == 1 ? wave_id : wave_id % kRowWaves;  // row wave
+    // Row wave.  Causal, 8 waves: waves w and w+4 share a SIMD and get row
+    // blocks w and 7 - w, so that the fully masked tiles each wave skips
+    // (see nt_w) add up to the same count on every SIMD.
+    const int wave = KS == 1 ? ((kMask && NW == 8 && p.causal && wave_id >= 4) ? 11 - wave_id : wave_id)
+                             : wave_id % kRowWaves;
     const int kgrp = KS == 1 ? 0 : wave_id / kRowWaves;        // KV group
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x, p.xcds);
@@ -818,11 +822,12 @@ void kf_attn_prefill_kernel(AttnParams p) {
     }
 
     // Keys this workgroup needs (blk_lim) and, per wave, the smallest row
-    // limit (below it no masking is needed).
-    int kvb = kv_len, blk_lim = kv_len, wave_min = kv_len;
+    // limit (below it no masking is needed) and the largest (from it on
+    // every score of the wave is masked).
+    int kvb = kv_len, blk_lim = kv_len, wave_min = kv_len, wave_max = kv_len;
     if constexpr (kMask) {
         kvb = batch_kv_len(p, grp);
-        blk_lim = wave_min = kvb;
+        blk_lim = wave_min = wave_max = kvb;
         if (p.causal) {
             const int q_len = p.q_len;
             const int r0 = rt * kPrefillRows, r1 = min(R, r0 + kPrefillRows) - 1;
@@ -833,8 +838,10 @@ void kf_attn_prefill_kernel(AttnParams p) {
             if (w0 < R) {
                 qi_range(w0, min(R, w0 + 32) - 1, q_len, lo, hi);
                 wave_min = row_kv_limit(p, kvb, lo);
+                wave_max = row_kv_limit(p, kvb, hi);
             } else {
                 wave_min = blk_lim;
+                wave_max = 0;
             }
         }
     }
@@ -847,6 +854,11 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const int kv_base = kgrp * ntiles * BC;
     const int kv_end = min(kv_base + ntiles * BC, blk_lim);
     if constexpr (KS > 1) wave_min = min(wave_min, kv_end) - kv_base;
+    // Tiles with a key visible to some row of this wave.  The later ones are
+    // fully masked for it: their scores would contribute exactly nothing, so
+    // the wave skips them and only takes part in the stage barriers and
+    // copies (one KV group; with several, every group runs all its tiles).
+    const int nt_w = (kMask && KS == 1) ? min(ntiles, (wave_max + BC - 1) / BC) : ntiles;
     char* const b0 = buf0 + kgrp * S::kStageBytes;  // this group's stage regions
     char* const b1 = buf1 + kgrp * S::kStageBytes;
     char* const b2 = Cfg::kBuffers == 3 ? buf2 + kgrp * S::kStageBytes : buf2;  // unused at 2
@@ -1100,12 +1112,13 @@ void kf_attn_prefill_kernel(AttnParams p) {
                 if (js < nstages) issue_stage(fill, js * SR);
             }
         }
+        if (t >= nt_w) return;  // wave-uniform; never for the unmasked kernel
         f32x16 sn[kNSB];
         qk(nxt, qf, sn);
         softmax_exp(sc, neg_m(), pp, st.l);
         pv(cur, pp, o);
         float mx = block_rowmax<kNSB>(sn);
-        if (t + 1 < ntiles) {
+        if (t + 1 < nt_w) {
             if ((t + 2) * BC > wave_min) {  // S(t+1) needs masking (tail / causal)
                 // Keep this a branch: if-converted, the compares and selects
                 // of the mask would run on every tile.
