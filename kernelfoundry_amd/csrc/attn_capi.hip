@@ -56,6 +56,9 @@ long long decode_stream_splits(long long n_groups, long long max_splits, int D, 
 constexpr long long kShortMaxWavesPerCU = 8;
 constexpr long long kShortMinWavesPerCU = 4;
 constexpr int kMinGroupKeys = 128;      // keys before a prefill row's keys are split between KV groups
+// Time per query row of the wide prefill kernel relative to the 256-row
+// kernel (measured at S = 4096, 32 / 8 heads: 254 vs 267-271 us).
+constexpr double kWideRowCost = 0.94;
 constexpr size_t kWsAlign = 256;
 
 thread_local int g_last_hip_error = 0;
@@ -106,6 +109,9 @@ struct Plan {
     int threads;
     int waves;          // prefill: waves per workgroup
     int kv_groups;      // prefill: KV groups per workgroup (1, 2 or 4)
+    int wide_row_tiles; // prefill without masking: 512-row tiles of the wide
+                        // kernel per KV head, 0 = the 32-row-per-wave kernel
+    int wide_grid;      // workgroups of the wide kernel
     int short_stages;   // decode: 32-key stages per split of the short-split kernel, 0 = streaming kernel
     int merge_cw;       // split merge: float4 columns per wave
     int merge_per;      // split merge: splits per lane
@@ -212,6 +218,21 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
         p.waves = nw;
         p.kv_groups = ks;
         p.path = KF_PATH_PREFILL;
+        // Unmasked calls at D = 64 / 128 with 8-wave workgroups: the wide
+        // kernel (64 rows per wave, 512 per workgroup) when its rounds of
+        // workgroups take less time than the 256-row kernel's; one workgroup
+        // runs per CU in either kernel, and a wide row costs kWideRowCost of
+        // a 256-row-kernel row.
+        if ((D == 64 || D == 128) && nw == 8 && ks == 1) {
+            const long long wrt = (R + kf::WideCfg<128>::kRows - 1) / kf::WideCfg<128>::kRows;
+            const long long wg = n_groups * wrt;
+            const long long rounds_n = (p.grid + cus - 1) / cus, rounds_w = (wg + cus - 1) / cus;
+            if (wg <= INT_MAX &&
+                (double)rounds_w * kf::WideCfg<128>::kRows * kWideRowCost < (double)rounds_n * rows) {
+                p.wide_row_tiles = (int)wrt;
+                p.wide_grid = (int)wg;
+            }
+        }
     }
     if (p.path == KF_PATH_DECODE_SPLIT) {
         const size_t parts = (size_t)p.n_splits * (size_t)rows_total;
@@ -256,6 +277,15 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
                         launch_prefill<D, 8, 2>(pl, prm, mask, stream);
                     else
                         launch_prefill<D, 4, 2>(pl, prm, mask, stream);
+                    return hipGetLastError();
+                }
+            }
+            if constexpr (D == 64 || D == 128) {
+                if (!mask && pl.wide_row_tiles > 0) {
+                    kf::AttnParams pw = prm;
+                    pw.row_tiles = pl.wide_row_tiles;
+                    kf::kf_attn_prefill_wide_kernel<D><<<dim3(pl.wide_grid), dim3(kf::WideCfg<D>::kThreads), 0,
+                                                         stream>>>(pw);
                     return hipGetLastError();
                 }
             }
@@ -462,7 +492,9 @@ int describe_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const 
     plan->rows_per_group = pl.R;
     plan->num_splits = pl.n_splits;
     plan->kv_per_split = pl.kv_per_split;
-    plan->grid_blocks = pl.grid;
+    // The unmasked dispatch (kf_attn_fwd); masked calls of kf_attn_fwd_ex
+    // run the 256-row kernel's grid.
+    plan->grid_blocks = pl.wide_row_tiles > 0 ? pl.wide_grid : pl.grid;
     plan->block_threads = pl.threads;
     plan->workspace_bytes = pl.ws_bytes;
     plan->splits_per_block = pl.path == KF_PATH_PREFILL ? 0 : pl.short_stages > 0 ? kf::kShortWaves : 1;
@@ -493,8 +525,11 @@ int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
     int n;
     if (pl.path == KF_PATH_PREFILL) {
         const bool mask = (flags & KF_ATTN_CAUSAL) || kv_lens;
-        n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_kernel<%d, %s, %d, %d>", D,
-                     mask ? "true" : "false", pl.waves, pl.kv_groups);
+        if (!mask && pl.wide_row_tiles > 0)
+            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d>", D);
+        else
+            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_kernel<%d, %s, %d, %d>", D,
+                         mask ? "true" : "false", pl.waves, pl.kv_groups);
     } else {
         if (pl.short_stages > 0)
             n = snprintf(tmp, sizeof(tmp), "kf_attn_decode_short_kernel<%d, %d>", D, pl.short_stages);

@@ -166,10 +166,16 @@ def test_plan_null_out(lib):
 # Dispatch plans for the BASELINE.json configs and the split geometry.
 # ---------------------------------------------------------------------------
 def test_plans_for_baseline_configs():
-    p = kf.plan(1, 4096, 4096, 32, 8, 128)           # C3 prefill
-    rows_per_block = p.block_threads // 64 * 32      # 32 query rows per wave
+    p = kf.plan(1, 4096, 4096, 32, 8, 128)           # C3 prefill: wide kernel,
     assert p.path == "prefill" and p.rows_per_group == 4 * 4096
-    assert p.grid_blocks == 8 * (4 * 4096 // rows_per_block)
+    assert p.block_threads == 512                    # 8 waves x 64 query rows
+    assert p.grid_blocks == 8 * (4 * 4096 // 512) == 256
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128>"
+    # masked: the 256-row kernel (8 waves x 32 rows), 512 workgroups
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == "kf_attn_prefill_kernel<128, true, 8, 1>"
+    p = kf.plan(1, 2048, 2048, 32, 8, 128)           # S = 2048: 128 wide workgroups would idle CUs
+    assert p.grid_blocks == 256
+    assert kf.kernel_names(1, 2048, 2048, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 1>"
     p = kf.plan(1, 512, 512, 32, 8, 128)             # C1: 64 8-wave blocks would idle CUs
     assert p.path == "prefill" and p.block_threads == 512  # 2 row waves x 4 KV groups
     assert p.grid_blocks == 8 * (4 * 512 // 64) == 256
@@ -257,11 +263,18 @@ def test_prefill_waves_per_workgroup(S, H_kv, D, waves, groups):
     D = 256)."""
     p = kf.plan(1, S, S, 32, H_kv, D)
     assert p.path == "prefill" and p.block_threads == 64 * waves
-    assert kf.kernel_names(1, S, S, 32, H_kv, D) == \
-        f"kf_attn_prefill_kernel<{D}, false, {waves}, {groups}>"
+    # Masked calls always run this kernel; unmasked ones may run the wide
+    # kernel instead (test_wide_prefill_selection).
+    assert kf.kernel_names(1, S, S, 32, H_kv, D, causal=True) == \
+        f"kf_attn_prefill_kernel<{D}, true, {waves}, {groups}>"
     rows = 32 * waves // groups
     R = 32 // H_kv * S
-    assert p.grid_blocks == H_kv * -(-R // rows)
+    if kf.kernel_names(1, S, S, 32, H_kv, D).startswith("kf_attn_prefill_wide_kernel"):
+        assert p.grid_blocks == H_kv * -(-R // 512)
+    else:
+        assert kf.kernel_names(1, S, S, 32, H_kv, D) == \
+            f"kf_attn_prefill_kernel<{D}, false, {waves}, {groups}>"
+        assert p.grid_blocks == H_kv * -(-R // rows)
     full = H_kv * -(-R // (256 if D <= 128 else 128)) >= 256
     if full:
         assert rows == (256 if D <= 128 else 128) and groups == 1
@@ -273,6 +286,33 @@ def test_prefill_waves_per_workgroup(S, H_kv, D, waves, groups):
         assert groups == 1
 
 
+@pytest.mark.parametrize("B,S,H_q,H_kv,D,cus", [
+    (1, 4096, 32, 8, 128, 256), (1, 2048, 32, 8, 128, 256), (1, 8192, 32, 8, 128, 256),
+    (1, 4096, 32, 8, 64, 256), (1, 2048, 32, 1, 64, 256), (32, 100, 32, 8, 128, 256),
+    (32, 130, 32, 8, 128, 256), (4, 1024, 64, 64, 128, 256), (1, 4096, 32, 8, 128, 80),
+    (1, 4096, 32, 8, 128, 32), (1, 4096, 32, 8, 256, 256), (1, 4096, 32, 8, 16, 256),
+    (3, 3000, 32, 8, 128, 304),
+])
+def test_wide_prefill_selection(B, S, H_q, H_kv, D, cus):
+    """Unmasked prefill at D = 64 / 128 runs the wide kernel (8 waves x 64
+    rows = 512 rows per workgroup) when the 256-row kernel would run 8-wave
+    workgroups without KV groups and the wide grid's rounds of one workgroup
+    per CU take less time, a wide row costing 0.94 of a 256-row-kernel row:
+    rounds(wide) * 512 * 0.94 < rounds(256-row) * 256."""
+    p = kf.plan(B, S, S, H_q, H_kv, D, num_cus=cus)
+    R = H_q // H_kv * S
+    n_groups = B * H_kv
+    narrow = n_groups * -(-R // 256)
+    wide = n_groups * -(-R // 512)
+    rounds = lambda w: -(-w // cus)
+    expect = (D in (64, 128) and narrow >= cus and
+              rounds(wide) * 512 * 0.94 < rounds(narrow) * 256)
+    if expect:
+        assert p.grid_blocks == wide and p.block_threads == 512
+    elif D in (64, 128) and narrow >= cus:
+        assert p.grid_blocks == narrow
+
+
 @pytest.mark.parametrize("cus", [32, 80, 256])
 def test_plans_scale_with_the_device_cu_count(cus):
     """kf_attn_plan_for_cus sizes the dispatch for `cus` compute units: the
@@ -282,14 +322,19 @@ def test_plans_scale_with_the_device_cu_count(cus):
     busiest CU is within 2 % of an even share."""
     # C1 prefill (S=512): 8 heads x 8 row tiles of 256 rows = 64 workgroups.
     p = kf.plan(1, 512, 512, 32, 8, 128, num_cus=cus)
-    if 64 >= cus:
+    rounds = lambda w: -(-w // cus)
+    if 64 >= cus and rounds(32) * 512 * 0.94 < rounds(64) * 256:
+        assert p.block_threads == 512 and p.grid_blocks == 32          # wide kernel, 512 rows
+    elif 64 >= cus:
         assert p.block_threads == 512 and p.grid_blocks == 64          # 8 waves, one KV group
     elif 8 * (4 * 512 // 128) >= cus:
         assert p.block_threads == 512 and p.grid_blocks == 128         # 2 KV groups, 128 rows
     else:
         assert p.block_threads == 512 and p.grid_blocks == 256         # 4 KV groups, 64 rows
-    # C3 prefill: 512 workgroups whatever the device.
-    assert kf.plan(1, 4096, 4096, 32, 8, 128, num_cus=cus).grid_blocks == 512
+    # C3 prefill: 256 wide workgroups, or 512 of the 256-row kernel where
+    # those take less time (80 CUs: 7 rounds of 256 rows against 4 of 512).
+    wide_c3 = rounds(256) * 512 * 0.94 < rounds(512) * 256
+    assert kf.plan(1, 4096, 4096, 32, 8, 128, num_cus=cus).grid_blocks == (256 if wide_c3 else 512)
     # C2 decode: short splits while 1024 one-wave splits fit 8 per CU.
     p = kf.plan(1, 1, 4096, 32, 8, 128, num_cus=cus)
     w64, w32 = 8 * 64, 8 * 128                   # waves of 64- and 32-key splits
@@ -330,7 +375,8 @@ def test_plan_for_cus_rejects_bad_counts(lib):
 def test_kernel_names_follow_the_plan(lib):
     """kf_attn_kernel_names names the kernels in launch order, as the
     profiler lists them."""
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128>"
+    assert kf.kernel_names(1, 2048, 2048, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 1>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == \
         "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, masked=True) == \

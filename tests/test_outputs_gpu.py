@@ -8,7 +8,8 @@ the bits are the references).  LSE must equal Mi + ln(Li) of the fp32 call
 (to the accuracy of the hardware log) and the fp64 oracle's
 Mi + ln(Li) to 1e-3; rows without keys give LSE = -inf.
 
-Every kernel path that writes O is covered: prefill (unmasked and masked),
+Every kernel path that writes O is covered: prefill (unmasked and masked, the
+256-row and the wide 512-row kernel),
 decode without split (O written by the decode kernel), decode with split
 (O written by the merge kernel), and paged decode.
 """
@@ -38,6 +39,7 @@ def _bf16_rne(x32):
 CASES = [
     # B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens       path
     (1, 8, 2, 300, 300, 128, False, None),                # prefill
+    (32, 32, 8, 100, 77, 128, False, None),               # wide prefill (512-row workgroups)
     (2, 8, 2, 200, 260, 64, True, [260, 0]),              # prefill, masked, empty sequence
     (1, 4, 4, 64, 64, 256, False, None),                  # prefill D=256
     (2, 8, 8, 1, 100, 16, False, None),                   # decode, one split

@@ -1,5 +1,6 @@
 """Property test of the dispatch planner (kf_attn_plan, host code only) over
-random shapes: every plan covers all keys of a head exactly once with whole
+random shapes: every prefill plan's row tiles cover the query rows of a
+head, every decode plan covers all keys of a head exactly once with whole
 32-key stages, stays within the split merge's one-pass capacity, gives the
 streaming decode kernel at least one stage per wave in each split, and sizes
 the split workspace for every partial."""
@@ -32,11 +33,13 @@ def test_plan_invariants(B, H_kv, ratio, q, kv, D, cus):
         waves = p.block_threads // 64
         assert waves in ((4,) if D == 256 else (2, 4, 8))
         # A workgroup holds 32 query rows per wave, or 32 per wave of one of
-        # its two or four KV groups (each taking that share of the keys); row
-        # tiles cover R.
+        # its two or four KV groups (each taking that share of the keys), or
+        # (the wide kernel, 8 waves at D = 64 / 128) 64 per wave; row tiles
+        # cover R.
         assert p.grid_blocks % n_groups == 0
         tiles = p.grid_blocks // n_groups
-        assert tiles in (-(-R // (32 * waves)), -(-R // (16 * waves)), -(-R // (8 * waves)))
+        wide = (-(-R // 512),) if (waves == 8 and D in (64, 128)) else ()
+        assert tiles in (-(-R // (32 * waves)), -(-R // (16 * waves)), -(-R // (8 * waves))) + wide
         assert p.workspace_bytes == 0 and p.num_splits == 1
         return
     assert R <= 32

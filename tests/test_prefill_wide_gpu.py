@@ -1,0 +1,93 @@
+"""GPU parity of the wide prefill kernel (8 waves x 64 query rows, 512 rows
+per workgroup; kf_attn_prefill_wide_kernel<D>) at D = 64 and 128.
+
+The planner runs it for unmasked calls when its grid of 512-row tiles
+finishes in fewer workgroup rounds than the 256-row kernel's; every shape
+here is chosen so that it does (asserted through kf.kernel_names), and so
+that its edge cases are hit: padding query rows (rows per KV head % 512 !=
+0, fewer than 512 rows), a ragged last tile (kv_len % 32 != 0), an odd tile
+count (the last 64-row stage holds one tile), a partial last stage, a single
+key, one to many stages, GQA ratios 1, 4 and 32, and several row tiles per KV
+head.  O, Mi and Li are compared with oracle/attn_oracle.py's fp64 ``sdpa``
+on the same fp16 inputs to the north-star bar (max |got - ref| <= 2e-3,
+||got - ref|| / ||ref|| <= 1e-2; Mi to 1e-4, Li to 1e-3 relative).
+
+The wide kernel computes every row with the same operation order as the
+256-row kernel, so its output must also equal, bit for bit, that kernel's on
+the same inputs (run through kf_attn_fwd_ex with every sequence's key count
+equal to kv_len, which selects the 256-row kernel's masked instantiation
+with no key masked).
+"""
+import numpy as np
+import pytest
+
+from oracle import attn_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    return torch
+
+
+CASES = [
+    # B, H_q, H_kv, q_len, kv_len, D           what it hits
+    (32, 32, 8, 100, 77, 128),     # 400 rows (< 512, padding), ragged tail, odd tiles, partial stage
+    (32, 32, 8, 100, 1, 128),      # one key: one tile, 31 keys masked
+    (16, 32, 8, 256, 160, 128),    # two row tiles per head, 2.5 stages
+    (4, 64, 64, 1024, 96, 128),    # MHA (ratio 1), 1.5 stages
+    (8, 32, 1, 512, 300, 128),     # MQA (ratio 32): 16384 rows, 32 row tiles, ragged
+    (4, 32, 8, 2048, 1000, 128),   # 16 row tiles per head, 16 stages, ragged
+    (32, 32, 8, 100, 77, 64),      # D = 64 (block-1 Q^T in registers)
+    (8, 32, 1, 512, 513, 64),      # D = 64 MQA, one key into the last stage
+]
+
+
+def _ids(c):
+    return "B{}_Hq{}_Hkv{}_q{}_kv{}_D{}".format(*c)
+
+
+def _inputs(B, H_q, H_kv, q_len, kv_len, D, seed):
+    torch = _torch()
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, q_len, kv_len, D, seed)
+    dev = (torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in (q16, k16, v16))
+    return (q16, k16, v16), tuple(dev)
+
+
+@pytest.mark.parametrize("case", CASES, ids=_ids)
+def test_wide_prefill_matches_oracle(case):
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    B, H_q, H_kv, q_len, kv_len, D = case
+    names = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D)
+    print("case", case, names, flush=True)
+    assert names == f"kf_attn_prefill_wide_kernel<{D}>", names
+    (q16, k16, v16), (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 11 + kv_len)
+    O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True)
+    torch.cuda.synchronize()
+    O, Mi, Li = O.cpu().numpy(), Mi.cpu().numpy(), Li.cpu().numpy()
+    Or, Mr, Lr = orc.sdpa(q16, k16, v16)
+    assert np.isfinite(O).all(), "non-finite O"
+    ok, max_abs, rel = orc.within_tolerance(O, Or)
+    assert ok, f"max_abs={max_abs:.3g} rel={rel:.3g}"
+    assert np.abs(Mi - Mr).max() <= 1e-4, "Mi"
+    assert (np.abs(Li - Lr) / np.abs(Lr)).max() <= 1e-3, "Li"
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[4], CASES[6]], ids=_ids)
+def test_wide_prefill_equals_256_row_kernel_bitwise(case):
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    B, H_q, H_kv, q_len, kv_len, D = case
+    masked = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, masked=True)
+    print("case", case, masked, flush=True)
+    assert masked == f"kf_attn_prefill_kernel<{D}, true, 8, 1>", masked
+    _, (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 5)
+    full = torch.full((B,), kv_len, dtype=torch.int32, device="cuda")
+    Ow, Mw, Lw = kf.attn_fwd(Q, K, V, return_stats=True)
+    On, Mn, Ln = kf.attn_fwd(Q, K, V, return_stats=True, kv_lens=full)
+    torch.cuda.synchronize()
+    assert torch.equal(Ow, On), f"O differs: max {(Ow - On).abs().max().item():.3g}"
+    assert torch.equal(Mw, Mn) and torch.equal(Lw, Ln), "Mi / Li differ"
