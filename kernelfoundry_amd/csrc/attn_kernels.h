@@ -1284,6 +1284,9 @@ template <int D> struct WideCfg {
     static constexpr int BC = 32;                  // kv rows per MFMA tile
     static constexpr int kStageRows = 64;          // kv rows per LDS stage
     static constexpr bool kQ1Lds = D >= 128;       // block-1 Q^T read from LDS
+    // S(t+1) overlapped with the softmax of tile t (a second score block per
+    // row block) where the registers allow it: D = 64.
+    static constexpr bool kPipe = D <= 64;
 };
 
 template <int D>
@@ -1296,6 +1299,7 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     constexpr int SR = Cfg::kStageRows;
     constexpr int kRows = Cfg::kRows;
     constexpr bool kQ1Lds = Cfg::kQ1Lds;
+    constexpr bool kPipe = Cfg::kPipe;
     using S = DmaStage<D, SR, NW>;
     using SW = SwizzleRow<D>;
     constexpr int kNKK = D / 16;
@@ -1303,6 +1307,7 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     constexpr int kHalfRows = kRows / 2;           // rows of one row block, all waves
     __shared__ __attribute__((aligned(1024))) char buf0[S::kStageBytes];
     __shared__ __attribute__((aligned(1024))) char buf1[S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char buf2[kPipe ? S::kStageBytes : 16];
     // The stage buffers come first (the backend orders LDS variables by
     // alignment), so their addresses fit the 16-bit immediate offset of the
     // LDS reads and no K / V read needs address arithmetic (measured +1.6 %).
@@ -1438,10 +1443,8 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
         o1[td] = f32x16{};
     }
 
-    // One 32-key tile: K rows at `stage`, V rows at stage + kTensorBytes;
-    // t is the tile index.
-    auto tile = [&](const char* stage, int t) {
-        f32x16 s0[1], s1[1];
+    // S^T of both row blocks for the tile whose K rows are at `stage`.
+    auto qk2 = [&](const char* stage, f32x16 (&s0)[1], f32x16 (&s1)[1]) {
         s0[0] = f32x16{};
         s1[0] = f32x16{};
 #pragma unroll
@@ -1455,11 +1458,13 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
                 qb = q1[kk];
             s1[0] = mfma32(kf, qb, s1[0]);
         }
-        if ((t + 1) * BC > kv_len) {  // tail tile: keys past kv_len
-            // Register r of lane l holds key 8 (r / 4) + 4 (l / 32) + r % 4
-            // of the tile: compare 8 (r / 4) + r % 4 (an inline constant)
-            // with the limit less 4 (l / 32), so no per-register key index
-            // stays live across the loop.
+    };
+    // Keys past kv_len in tile t (the last tile) -> -inf.  Register r of
+    // lane l holds key 8 (r / 4) + 4 (l / 32) + r % 4 of the tile: compare
+    // 8 (r / 4) + r % 4 (an inline constant) with the limit less 4 (l / 32),
+    // so no per-register key index stays live across the loop.
+    auto tail_mask = [&](f32x16 (&s0)[1], f32x16 (&s1)[1], int t) {
+        if ((t + 1) * BC > kv_len) {
             asm volatile("" ::: "memory");
             const int lg = kv_len - t * BC - 4 * g;
 #pragma unroll
@@ -1469,11 +1474,9 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
                     s1[0][r] = -INFINITY;
                 }
         }
-        f16x8 p0[2], p1[2];
-        block_update_max<kNTD>(st0, block_rowmax<1>(s0), c, inv_c, o0);
-        block_exp(s0[0], c, -st0.m, p0[0], p0[1], st0.l);
-        block_update_max<kNTD>(st1, block_rowmax<1>(s1), c, inv_c, o1);
-        block_exp(s1[0], c, -st1.m, p1[0], p1[1], st1.l);
+    };
+    // O^T += V^T P^T for both row blocks, V rows at stage + kTensorBytes.
+    auto pv2 = [&](const char* stage, const f16x8 (&p0)[2], const f16x8 (&p1)[2]) {
 #pragma unroll
         for (int td = 0; td < kNTD; ++td)
 #pragma unroll
@@ -1485,22 +1488,88 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
                 o1[td] = mfma32(a, p1[jj], o1[td]);
             }
     };
-
     constexpr int H = BC * S::kRowBytes;  // bytes of one tile's K (or V) rows
-    for (int js = 0; js < nstages; js += 2) {
+
+    if constexpr (!kPipe) {
+        // One 32-key tile at `stage`: S^T of both blocks, the row max / lazy
+        // rescale / exp2 of each, then P.V for both.
+        auto tile = [&](const char* stage, int t) {
+            f32x16 s0[1], s1[1];
+            qk2(stage, s0, s1);
+            tail_mask(s0, s1, t);
+            f16x8 p0[2], p1[2];
+            block_update_max<kNTD>(st0, block_rowmax<1>(s0), c, inv_c, o0);
+            block_exp(s0[0], c, -st0.m, p0[0], p0[1], st0.l);
+            block_update_max<kNTD>(st1, block_rowmax<1>(s1), c, inv_c, o1);
+            block_exp(s1[0], c, -st1.m, p1[0], p1[1], st1.l);
+            pv2(stage, p0, p1);
+        };
+        for (int js = 0; js < nstages; js += 2) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int j = js + u;
-            if (j >= nstages) break;
-            char* cur = u == 0 ? buf0 : buf1;
-            char* nxt = u == 0 ? buf1 : buf0;
-            // Stage j (and, at j = 0, the block-1 query rows) landed for
-            // every wave; every wave is done with stage j-1 (in nxt).
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (j + 1 < nstages) issue_stage(nxt, (j + 1) * SR);
-            tile(cur, 2 * j);
-            if (2 * j + 1 < ntiles) tile(cur + H, 2 * j + 1);
+            for (int u = 0; u < 2; ++u) {
+                const int j = js + u;
+                if (j >= nstages) break;
+                char* cur = u == 0 ? buf0 : buf1;
+                char* nxt = u == 0 ? buf1 : buf0;
+                // Stage j (and, at j = 0, the block-1 query rows) landed for
+                // every wave; every wave is done with stage j-1 (in nxt).
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                if (j + 1 < nstages) issue_stage(nxt, (j + 1) * SR);
+                tile(cur, 2 * j);
+                if (2 * j + 1 < ntiles) tile(cur + H, 2 * j + 1);
+            }
+        }
+    } else {
+        // Pipelined as kf_attn_prefill_kernel's 8-wave layout: S(t+1) of both
+        // blocks is computed while tile t's scores are exponentiated, then
+        // P.V(t) and the row max of S(t+1).  Tile t reads V(t) from `cur`
+        // and K(t+1) from `nxt`, which may be the next stage: three buffers,
+        // the copy of stage j+2 issued at the barrier before the last tile of
+        // stage j (stage j-1 is then free and stage j+1 has landed).
+        if (nstages > 1) issue_stage(buf1, SR);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        f32x16 sc0[1], sc1[1];
+        qk2(buf0, sc0, sc1);
+        tail_mask(sc0, sc1, 0);
+        block_update_max<kNTD>(st0, block_rowmax<1>(sc0), c, inv_c, o0);
+        block_update_max<kNTD>(st1, block_rowmax<1>(sc1), c, inv_c, o1);
+        auto tile = [&](char* cur, char* nxt, char* fill, int t, bool sync) {
+            if (sync) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                const int js = t / 2 + 2;
+                if (js < nstages) issue_stage(fill, js * SR);
+            }
+            f32x16 sn0[1], sn1[1];
+            qk2(nxt, sn0, sn1);  // the last tile's reads a stale buffer, discarded
+            f16x8 p0[2], p1[2];
+            block_exp(sc0[0], c, -st0.m, p0[0], p0[1], st0.l);
+            block_exp(sc1[0], c, -st1.m, p1[0], p1[1], st1.l);
+            pv2(cur, p0, p1);
+            if (t + 1 < ntiles) {
+                tail_mask(sn0, sn1, t + 1);
+                block_update_max<kNTD>(st0, block_rowmax<1>(sn0), c, inv_c, o0);
+                block_update_max<kNTD>(st1, block_rowmax<1>(sn1), c, inv_c, o1);
+                sc0[0] = sn0[0];
+                sc1[0] = sn1[0];
+            }
+        };
+        // Tile t reads the (t % 2)-th half of stage t / 2, which lives in
+        // buffer (t / 2) % 3; the loop body covers 3 stages.
+        for (int t = 0; t < ntiles; t += 6) {
+            tile(buf0, buf0 + H, nullptr, t, false);
+            if (t + 1 >= ntiles) break;
+            tile(buf0 + H, buf1, buf2, t + 1, true);
+            if (t + 2 >= ntiles) break;
+            tile(buf1, buf1 + H, nullptr, t + 2, false);
+            if (t + 3 >= ntiles) break;
+            tile(buf1 + H, buf2, buf0, t + 3, true);
+            if (t + 4 >= ntiles) break;
+            tile(buf2, buf2 + H, nullptr, t + 4, false);
+            if (t + 5 >= ntiles) break;
+            tile(buf2 + H, buf0, buf1, t + 5, true);
         }
     }
 
