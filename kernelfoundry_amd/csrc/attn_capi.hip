@@ -59,6 +59,9 @@ constexpr int kMinGroupKeys = 128;      // keys before a prefill row's keys are 
 // Time per query row of the wide prefill kernel relative to the 256-row
 // kernel (measured at S = 4096, 32 / 8 heads: 254 vs 267-271 us).
 constexpr double kWideRowCost = 0.94;
+// The same for the 8-wave D = 256 kernel (256 rows per workgroup) against the
+// 4-wave one (128 rows): 487 vs 689 us at S = 4096, 32 / 8 heads.
+constexpr double kWide256RowCost = 0.7;
 constexpr size_t kWsAlign = 256;
 
 thread_local int g_last_hip_error = 0;
@@ -222,13 +225,16 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
         // kernel (64 rows per wave, 512 per workgroup) when its rounds of
         // workgroups take less time than the 256-row kernel's; one workgroup
         // runs per CU in either kernel, and a wide row costs kWideRowCost of
-        // a 256-row-kernel row.
-        if ((D == 64 || D == 128) && nw == 8 && ks == 1) {
-            const long long wrt = (R + kf::WideCfg<128>::kRows - 1) / kf::WideCfg<128>::kRows;
+        // a 256-row-kernel row.  D = 256: the wide kernel's 8 waves x 32 rows
+        // against 4 waves x 32 rows, by the same rule (kWide256RowCost).
+        const bool wide_ok = ((D == 64 || D == 128) && nw == 8 && ks == 1) || (D == 256 && nw == 4);
+        if (wide_ok) {
+            const int wrows = D >= 256 ? kf::WideCfg<256>::kRows : kf::WideCfg<128>::kRows;
+            const double wcost = D >= 256 ? kWide256RowCost : kWideRowCost;
+            const long long wrt = (R + wrows - 1) / wrows;
             const long long wg = n_groups * wrt;
             const long long rounds_n = (p.grid + cus - 1) / cus, rounds_w = (wg + cus - 1) / cus;
-            if (wg <= INT_MAX &&
-                (double)rounds_w * kf::WideCfg<128>::kRows * kWideRowCost < (double)rounds_n * rows) {
+            if (wg <= INT_MAX && (double)rounds_w * wrows * wcost < (double)rounds_n * rows) {
                 p.wide_row_tiles = (int)wrt;
                 p.wide_grid = (int)wg;
             }
@@ -265,6 +271,13 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
     if (pl.path == KF_PATH_PREFILL) {
         const bool mask = prm.causal || prm.kv_lens;
         if constexpr (D >= 256) {
+            if (!mask && pl.wide_row_tiles > 0) {
+                kf::AttnParams pw = prm;
+                pw.row_tiles = pl.wide_row_tiles;
+                kf::kf_attn_prefill_wide_kernel<D><<<dim3(pl.wide_grid), dim3(kf::WideCfg<D>::kThreads), 0,
+                                                     stream>>>(pw);
+                return hipGetLastError();
+            }
             launch_prefill<D, 4>(pl, prm, mask, stream);
         } else {
             if constexpr (D == 64 || D == 128) {
@@ -495,7 +508,7 @@ int describe_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const 
     // The unmasked dispatch (kf_attn_fwd); masked calls of kf_attn_fwd_ex
     // run the 256-row kernel's grid.
     plan->grid_blocks = pl.wide_row_tiles > 0 ? pl.wide_grid : pl.grid;
-    plan->block_threads = pl.threads;
+    plan->block_threads = pl.wide_row_tiles > 0 ? kf::WideCfg<128>::kThreads : pl.threads;
     plan->workspace_bytes = pl.ws_bytes;
     plan->splits_per_block = pl.path == KF_PATH_PREFILL ? 0 : pl.short_stages > 0 ? kf::kShortWaves : 1;
     return KF_OK;

@@ -1262,8 +1262,10 @@ void kf_attn_prefill_kernel(AttnParams p) {
 
 // ---------------------------------------------------------------------------
 // Wide prefill: 8 waves x 64 query rows (two 32-row blocks per wave) = 512
-// rows per workgroup, D = 64 / 128, unmasked (keys past kv_len in the last
-// tile are masked).  Each K fragment read from LDS feeds the S^T MFMAs of
+// rows per workgroup at D = 64 / 128, 8 waves x 32 rows at D = 256 (two waves
+// per SIMD where kf_attn_prefill_kernel runs one: 487 vs 689 us at S = 4096,
+// 32 / 8 heads, bit-identical); unmasked (keys past kv_len in the last tile
+// are masked).  Each K fragment read from LDS feeds the S^T MFMAs of
 // both row blocks and each V^T fragment the O^T MFMAs of both, so LDS reads,
 // LDS-DMA bytes and workgroup barriers per MFMA are half those of the
 // 32-row kf_attn_prefill_kernel (measured at S = 4096, 32 / 8 heads: 6 %
@@ -1280,19 +1282,25 @@ void kf_attn_prefill_kernel(AttnParams p) {
 template <int D> struct WideCfg {
     static constexpr int kWaves = 8;
     static constexpr int kThreads = 64 * kWaves;
-    static constexpr int kRows = 64 * kWaves;      // query rows per workgroup
-    static constexpr int BC = 32;                  // kv rows per MFMA tile
-    static constexpr int kStageRows = 64;          // kv rows per LDS stage
-    static constexpr bool kQ1Lds = D >= 128;       // block-1 Q^T read from LDS
+    // 32-row blocks per wave: two at D <= 128; one at D = 256, whose 128 fp32
+    // O accumulators per block leave no room for a second.
+    static constexpr int kRB = D >= 256 ? 1 : 2;
+    static constexpr int kRows = 32 * kRB * kWaves;             // query rows per workgroup
+    static constexpr int BC = 32;                               // kv rows per MFMA tile
+    static constexpr int kStageRows = D >= 256 ? 32 : 64;       // kv rows per LDS stage
+    static constexpr bool kQ1Lds = D == 128;                    // block-1 Q^T read from LDS
     // S(t+1) overlapped with the softmax of tile t (a second score block per
     // row block) where the registers allow it: D = 64.
     static constexpr bool kPipe = D <= 64;
+    // D = 256: the per-lane LDS read offsets (16 for K, 16 for V) are derived
+    // at each tile from one base each by XOR, not held in 32 registers.
+    static constexpr bool kXorOff = D >= 256;
 };
 
 template <int D>
 __global__ __launch_bounds__(WideCfg<D>::kThreads, 2)
 void kf_attn_prefill_wide_kernel(AttnParams p) {
-    static_assert(D == 64 || D == 128, "wide prefill: D = 64 or 128");
+    static_assert(D == 64 || D == 128 || D == 256, "wide prefill: D = 64, 128 or 256");
     using Cfg = WideCfg<D>;
     constexpr int NW = Cfg::kWaves;
     constexpr int BC = Cfg::BC;
@@ -1300,6 +1308,8 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     constexpr int kRows = Cfg::kRows;
     constexpr bool kQ1Lds = Cfg::kQ1Lds;
     constexpr bool kPipe = Cfg::kPipe;
+    constexpr int kRB = Cfg::kRB;
+    constexpr bool kXorOff = Cfg::kXorOff;
     using S = DmaStage<D, SR, NW>;
     using SW = SwizzleRow<D>;
     constexpr int kNKK = D / 16;
@@ -1403,6 +1413,13 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             }
     }
 
+    // kXorOff: with phys chunk (2 kk + g) ^ h(r) = 2 kk ^ (g ^ h(r)), the K
+    // offset of k-step kk is koff[0] ^ 32 kk; the V^T offsets are voff[0][0]
+    // ^ 64 td for the first 8 rows and, since h(r + 8) = h(r) ^ 8 (D = 128 /
+    // 256 swizzle), that ^ 128, plus 8 rows, for the second.
+    static_assert(!kXorOff || D >= 128, "XOR offsets use the D >= 128 swizzle");
+    const int kbase = koff[0], vbase = voff[0][0];
+
     // Row blocks: block 0 = rows [rt kRows + 32 w, + 32), block 1 = the same
     // in the second half of the workgroup's rows.  Rows past R compute on
     // row R - 1 and are never stored.
@@ -1410,7 +1427,7 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     const int row1 = row0 + kHalfRows;
 
     issue_stage(buf0, 0);
-    f16x8 q0[kNKK], q1[kQ1Lds ? 1 : kNKK];
+    f16x8 q0[kNKK], q1[(kRB == 2 && !kQ1Lds) ? kNKK : 1];
     load_q_frags<D>(Qg, row0, R, lane, q0);
     if constexpr (kQ1Lds) {
         // LDS-DMA of rows [rt kRows + kHalfRows, + kHalfRows) (rows past R
@@ -1428,7 +1445,7 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
                                  (uint32_t)((((lane % S::kChunks) ^ SW::h(r)) % S::kChunks) * 16);
             __builtin_amdgcn_global_load_lds(Qb + off, (lds_void*)(q1_lds + j * 1024), 16, 0, 0);
         }
-    } else {
+    } else if constexpr (kRB == 2) {
         load_q_frags<D>(Qg, row1, R, lane, q1);
     }
     const char* q1w = q1_lds + wave * 32 * S::kRowBytes;  // this wave's block-1 rows
@@ -1446,17 +1463,22 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     // S^T of both row blocks for the tile whose K rows are at `stage`.
     auto qk2 = [&](const char* stage, f32x16 (&s0)[1], f32x16 (&s1)[1]) {
         s0[0] = f32x16{};
-        s1[0] = f32x16{};
+        if constexpr (kRB == 2) s1[0] = f32x16{};
+        int kb = kbase;
+        if constexpr (kXorOff) asm volatile("" : "+v"(kb));  // recomputed per tile
 #pragma unroll
         for (int kk = 0; kk < kNKK; ++kk) {
-            const f16x8 kf = *reinterpret_cast<const f16x8*>(stage + koff[kk]);
+            const int ko = kXorOff ? (kb ^ (32 * kk)) : koff[kk];
+            const f16x8 kf = *reinterpret_cast<const f16x8*>(stage + ko);
             s0[0] = mfma32(kf, q0[kk], s0[0]);
-            f16x8 qb;
-            if constexpr (kQ1Lds)
-                qb = *reinterpret_cast<const f16x8*>(q1w + koff[kk]);
-            else
-                qb = q1[kk];
-            s1[0] = mfma32(kf, qb, s1[0]);
+            if constexpr (kRB == 2) {
+                f16x8 qb;
+                if constexpr (kQ1Lds)
+                    qb = *reinterpret_cast<const f16x8*>(q1w + koff[kk]);
+                else
+                    qb = q1[kk];
+                s1[0] = mfma32(kf, qb, s1[0]);
+            }
         }
     };
     // Keys past kv_len in tile t (the last tile) -> -inf.  Register r of
@@ -1471,22 +1493,27 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             for (int r = 0; r < 16; ++r)
                 if (8 * (r >> 2) + (r & 3) >= lg) {
                     s0[0][r] = -INFINITY;
-                    s1[0][r] = -INFINITY;
+                    if constexpr (kRB == 2) s1[0][r] = -INFINITY;
                 }
         }
     };
     // O^T += V^T P^T for both row blocks, V rows at stage + kTensorBytes.
     auto pv2 = [&](const char* stage, const f16x8 (&p0)[2], const f16x8 (&p1)[2]) {
+        int vb = vbase;
+        if constexpr (kXorOff) asm volatile("" : "+v"(vb));  // recomputed per tile
 #pragma unroll
-        for (int td = 0; td < kNTD; ++td)
+        for (int td = 0; td < kNTD; ++td) {
+            const int vo0 = kXorOff ? (vb ^ (64 * td)) : voff[td][0];
+            const int vo1 = kXorOff ? ((vb ^ (64 * td) ^ 128) + 8 * S::kRowBytes) : voff[td][1];
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
-                const f16x4 lo = lds_read_tr16(stage + voff[td][0] + jj * 16 * S::kRowBytes);
-                const f16x4 hi = lds_read_tr16(stage + voff[td][1] + jj * 16 * S::kRowBytes);
+                const f16x4 lo = lds_read_tr16(stage + vo0 + jj * 16 * S::kRowBytes);
+                const f16x4 hi = lds_read_tr16(stage + vo1 + jj * 16 * S::kRowBytes);
                 const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 o0[td] = mfma32(a, p0[jj], o0[td]);
-                o1[td] = mfma32(a, p1[jj], o1[td]);
+                if constexpr (kRB == 2) o1[td] = mfma32(a, p1[jj], o1[td]);
             }
+        }
     };
     constexpr int H = BC * S::kRowBytes;  // bytes of one tile's K (or V) rows
 
@@ -1500,10 +1527,14 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             f16x8 p0[2], p1[2];
             block_update_max<kNTD>(st0, block_rowmax<1>(s0), c, inv_c, o0);
             block_exp(s0[0], c, -st0.m, p0[0], p0[1], st0.l);
-            block_update_max<kNTD>(st1, block_rowmax<1>(s1), c, inv_c, o1);
-            block_exp(s1[0], c, -st1.m, p1[0], p1[1], st1.l);
+            if constexpr (kRB == 2) {
+                block_update_max<kNTD>(st1, block_rowmax<1>(s1), c, inv_c, o1);
+                block_exp(s1[0], c, -st1.m, p1[0], p1[1], st1.l);
+            }
             pv2(stage, p0, p1);
         };
+        constexpr int kSub = SR / BC;  // tiles per stage
+        static_assert(kSub == 1 || kSub == 2, "one or two tiles per stage");
         for (int js = 0; js < nstages; js += 2) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
@@ -1516,8 +1547,8 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
                 if (j + 1 < nstages) issue_stage(nxt, (j + 1) * SR);
-                tile(cur, 2 * j);
-                if (2 * j + 1 < ntiles) tile(cur + H, 2 * j + 1);
+                tile(cur, kSub * j);
+                if (kSub == 2 && 2 * j + 1 < ntiles) tile(cur + H, 2 * j + 1);
             }
         }
     } else {
@@ -1574,13 +1605,14 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     }
 
     // ---- Epilogue: both row blocks (every row saw key 0, so l > 0). ----
-    const float l0 = sum_xor32(st0.l), l1 = sum_xor32(st1.l);
+    const float l0 = sum_xor32(st0.l);
     if (row0 < R) {
         const size_t ri = (size_t)grp * R + row0;
         store_o_row_any<D>(p, ri, o0, 1.0f / l0, g);
         if (g == 0) store_stats(p, ri, st0.rmax * p.scale, l0 * exp2_hw(st0.m - st0.rmax * p.scale_log2));
     }
-    if (row1 < R) {
+    if (kRB == 2 && row1 < R) {
+        const float l1 = sum_xor32(st1.l);
         const size_t ri = (size_t)grp * R + row1;
         store_o_row_any<D>(p, ri, o1, 1.0f / l1, g);
         if (g == 0) store_stats(p, ri, st1.rmax * p.scale, l1 * exp2_hw(st1.m - st1.rmax * p.scale_log2));

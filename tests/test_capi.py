@@ -262,15 +262,16 @@ def test_prefill_waves_per_workgroup(S, H_kv, D, waves, groups):
     4 waves x 64 rows; the remaining cases halve the waves (down to 2, or 4 at
     D = 256)."""
     p = kf.plan(1, S, S, 32, H_kv, D)
-    assert p.path == "prefill" and p.block_threads == 64 * waves
+    wide = kf.kernel_names(1, S, S, 32, H_kv, D).startswith("kf_attn_prefill_wide_kernel")
+    assert p.path == "prefill" and p.block_threads == (512 if wide else 64 * waves)
     # Masked calls always run this kernel; unmasked ones may run the wide
     # kernel instead (test_wide_prefill_selection).
     assert kf.kernel_names(1, S, S, 32, H_kv, D, causal=True) == \
         f"kf_attn_prefill_kernel<{D}, true, {waves}, {groups}>"
     rows = 32 * waves // groups
     R = 32 // H_kv * S
-    if kf.kernel_names(1, S, S, 32, H_kv, D).startswith("kf_attn_prefill_wide_kernel"):
-        assert p.grid_blocks == H_kv * -(-R // 512)
+    if wide:
+        assert p.grid_blocks == H_kv * -(-R // (256 if D == 256 else 512))
     else:
         assert kf.kernel_names(1, S, S, 32, H_kv, D) == \
             f"kf_attn_prefill_kernel<{D}, false, {waves}, {groups}>"
@@ -298,18 +299,20 @@ def test_wide_prefill_selection(B, S, H_q, H_kv, D, cus):
     rows = 512 rows per workgroup) when the 256-row kernel would run 8-wave
     workgroups without KV groups and the wide grid's rounds of one workgroup
     per CU take less time, a wide row costing 0.94 of a 256-row-kernel row:
-    rounds(wide) * 512 * 0.94 < rounds(256-row) * 256."""
+    rounds(wide) * 512 * 0.94 < rounds(256-row) * 256.  D = 256: 8 waves x
+    32 rows against the 4-wave kernel's 128 rows, a row costing 0.7."""
     p = kf.plan(B, S, S, H_q, H_kv, D, num_cus=cus)
     R = H_q // H_kv * S
     n_groups = B * H_kv
-    narrow = n_groups * -(-R // 256)
-    wide = n_groups * -(-R // 512)
+    nrows, wrows, cost = (128, 256, 0.7) if D == 256 else (256, 512, 0.94)
+    narrow = n_groups * -(-R // nrows)
+    wide = n_groups * -(-R // wrows)
     rounds = lambda w: -(-w // cus)
-    expect = (D in (64, 128) and narrow >= cus and
-              rounds(wide) * 512 * 0.94 < rounds(narrow) * 256)
+    expect = (D in (64, 128, 256) and narrow >= cus and
+              rounds(wide) * wrows * cost < rounds(narrow) * nrows)
     if expect:
         assert p.grid_blocks == wide and p.block_threads == 512
-    elif D in (64, 128) and narrow >= cus:
+    elif D in (64, 128, 256) and narrow >= cus:
         assert p.grid_blocks == narrow
 
 
@@ -383,7 +386,8 @@ def test_kernel_names_follow_the_plan(lib):
         "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 512, 512, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 4>"
     assert kf.kernel_names(1, 256, 256, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 4, 2>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_kernel<256, false, 4, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_wide_kernel<256>"
+    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256) == "kf_attn_prefill_kernel<256, false, 4, 1>"
     assert kf.kernel_names(1, 1, 4096, 32, 8, 128) == \
         "kf_attn_decode_short_kernel<128, 1> + kf_attn_split_merge_kernel<128, 8, 4>"
     assert kf.kernel_names(32, 1, 8192, 32, 8, 128) == "kf_attn_decode_kernel<128, false>"

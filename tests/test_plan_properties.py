@@ -31,7 +31,7 @@ def test_plan_invariants(B, H_kv, ratio, q, kv, D, cus):
     if p.path == "prefill":
         assert R > 32
         waves = p.block_threads // 64
-        assert waves in ((4,) if D == 256 else (2, 4, 8))
+        assert waves in ((4, 8) if D == 256 else (2, 4, 8))
         # A workgroup holds 32 query rows per wave, or 32 per wave of one of
         # its two or four KV groups (each taking that share of the keys), or
         # (the wide kernel, 8 waves at D = 64 / 128) 64 per wave; row tiles

@@ -1,22 +1,24 @@
-"""GPU parity of the wide prefill kernel (8 waves x 64 query rows, 512 rows
-per workgroup; kf_attn_prefill_wide_kernel<D>) at D = 64 and 128.
+"""GPU parity of the wide prefill kernel (kf_attn_prefill_wide_kernel<D>: 8
+waves x 64 query rows, 512 rows per workgroup, at D = 64 and 128; 8 waves x
+32 rows at D = 256).
 
-The planner runs it for unmasked calls when its grid of 512-row tiles
-finishes in fewer workgroup rounds than the 256-row kernel's; every shape
+The planner runs it for unmasked calls when its grid finishes in less time
+than the narrower kernel's (rounds of one workgroup per CU); every shape
 here is chosen so that it does (asserted through kf.kernel_names), and so
 that its edge cases are hit: padding query rows (rows per KV head % 512 !=
 0, fewer than 512 rows), a ragged last tile (kv_len % 32 != 0), an odd tile
 count (the last 64-row stage holds one tile), a partial last stage, a single
-key, one to many stages, GQA ratios 1, 4 and 32, and several row tiles per KV
-head.  O, Mi and Li are compared with oracle/attn_oracle.py's fp64 ``sdpa``
-on the same fp16 inputs to the north-star bar (max |got - ref| <= 2e-3,
-||got - ref|| / ||ref|| <= 1e-2; Mi to 1e-4, Li to 1e-3 relative).
+key, one to many stages, GQA ratios 1, 4 and 32, several row tiles per KV
+head, and D = 256 with its LDS offsets derived by XOR.  O, Mi and Li are
+compared with oracle/attn_oracle.py's fp64 ``sdpa`` on the same fp16 inputs
+to the north-star bar (max |got - ref| <= 2e-3, ||got - ref|| / ||ref|| <=
+1e-2; Mi to 1e-4, Li to 1e-3 relative).
 
 The wide kernel computes every row with the same operation order as the
-256-row kernel, so its output must also equal, bit for bit, that kernel's on
-the same inputs (run through kf_attn_fwd_ex with every sequence's key count
-equal to kv_len, which selects the 256-row kernel's masked instantiation
-with no key masked).
+256-row kernel (the 128-row 4-wave kernel at D = 256), so its output must
+also equal, bit for bit, that kernel's on the same inputs (run through
+kf_attn_fwd_ex with every sequence's key count equal to kv_len, which selects
+that kernel's masked instantiation with no key masked).
 """
 import numpy as np
 import pytest
@@ -42,6 +44,9 @@ CASES = [
     (4, 32, 8, 2048, 1000, 128),   # 16 row tiles per head, 16 stages, ragged
     (32, 32, 8, 100, 77, 64),      # D = 64 (block-1 Q^T in registers)
     (8, 32, 1, 512, 513, 64),      # D = 64 MQA, one key into the last stage
+    (16, 16, 8, 150, 333, 256),    # D = 256 (8 waves x 32 rows): 300 rows, ragged
+    (8, 8, 8, 1024, 65, 256),      # D = 256 MHA, one key in the last tile
+    (8, 32, 1, 256, 200, 256),     # D = 256 MQA, 32 row tiles per head
 ]
 
 
@@ -76,14 +81,16 @@ def test_wide_prefill_matches_oracle(case):
     assert (np.abs(Li - Lr) / np.abs(Lr)).max() <= 1e-3, "Li"
 
 
-@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[4], CASES[6]], ids=_ids)
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[4], CASES[6], CASES[8], CASES[10]],
+                         ids=_ids)
 def test_wide_prefill_equals_256_row_kernel_bitwise(case):
     import kernelfoundry_amd as kf
     torch = _torch()
     B, H_q, H_kv, q_len, kv_len, D = case
     masked = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, masked=True)
     print("case", case, masked, flush=True)
-    assert masked == f"kf_attn_prefill_kernel<{D}, true, 8, 1>", masked
+    waves = 4 if D == 256 else 8
+    assert masked == f"kf_attn_prefill_kernel<{D}, true, {waves}, 1>", masked
     _, (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 5)
     full = torch.full((B,), kv_len, dtype=torch.int32, device="cuda")
     Ow, Mw, Lw = kf.attn_fwd(Q, K, V, return_stats=True)
