@@ -5,7 +5,9 @@ run: every key is zero except the last one, whose score exceeds all others
 by ~90 (e^-90 underflows the fp16 P to 0), so every output row must equal
 the last V row exactly, while every other V row holds -1; Mi must be that
 score and Li exactly 1.  A wrapped or truncated offset would read another
-row and show up as -1 / a wrong Mi."""
+row and show up as -1 / a wrong Mi.  Run through the decode kernels, the
+small-grid prefill and (65792 / 32896 query rows) the wide prefill kernel
+at D = 128 and 256."""
 import math
 
 import pytest
@@ -16,11 +18,15 @@ import kernelfoundry_amd as kf
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("q_len,H_q,D", [(1, 8, 128), (64, 1, 128), (1, 8, 256)])
+@pytest.mark.parametrize("q_len,H_q,D", [(1, 8, 128), (64, 1, 128), (1, 8, 256),
+                                         (2056, 32, 128), (1028, 32, 256)])
 def test_last_key_at_the_offset_limit(q_len, H_q, D):
     kv = (2 ** 31 - 1) // D // 64 * 64 - 64
-    print("case", dict(q_len=q_len, H_q=H_q, D=D, kv=kv, path=kf.plan(1, q_len, kv, H_q, 1, D).path),
-          flush=True)
+    names = kf.kernel_names(1, q_len, kv, H_q, 1, D)
+    print("case", dict(q_len=q_len, H_q=H_q, D=D, kv=kv, path=kf.plan(1, q_len, kv, H_q, 1, D).path,
+                       kernels=names), flush=True)
+    if q_len > 1000:  # 65792 / 32896 rows: the wide prefill kernel
+        assert names.startswith("kf_attn_prefill_wide_kernel"), names
     dev = torch.device("cuda")
     K = torch.zeros((1, 1, kv, D), dtype=torch.float16, device=dev)
     V = torch.full((1, 1, kv, D), -1.0, dtype=torch.float16, device=dev)
