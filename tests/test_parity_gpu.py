@@ -8,8 +8,10 @@ Tolerance: max |got - ref| <= 2e-3 AND
 ||got - ref||_2 / ||ref||_2 <= 1e-2, for O.  Mi (max scaled score) to
 1e-4 absolute and Li (sum of exp) to 1e-3 relative.
 
-Large configs (S=4096 prefill, B=32 x KV=8192 decode) are checked exactly on
-sampled (b, h) heads plus size-independent properties on every head.
+The BASELINE.json configs run at full size (S=4096 prefill, B=32 x KV=8192
+decode, 128 K / 256 K-key decode): every (b, h) head is compared with the
+oracle, plus size-independent properties (finite, Li >= 1, each output row
+inside the per-column range of its V rows).
 """
 import numpy as np
 import pytest
@@ -202,15 +204,6 @@ def _property_checks(O, Mi, Li, v16, H_q, H_kv):
     assert (O >= vmin - 1e-3).all() and (O <= vmax + 1e-3).all()
 
 
-def _sampled_heads_check(O, Mi, Li, q16, k16, v16, heads):
-    for b, h in heads:
-        H_q, H_kv = q16.shape[1], k16.shape[1]
-        hk = h // (H_q // H_kv)
-        Or, Mr, Lr = orc.sdpa(q16[b:b + 1, h:h + 1], k16[b:b + 1, hk:hk + 1], v16[b:b + 1, hk:hk + 1])
-        _check(O[b:b + 1, h:h + 1], Or, f"head b={b} h={h}")
-        _check_stats(Mi[b:b + 1, h:h + 1], Li[b:b + 1, h:h + 1], Mr, Lr, f"head b={b} h={h}")
-
-
 def _all_heads_check(O, Mi, Li, q16, k16, v16, what):
     """Every (b, h) head against the fp64 oracle on the same fp16 inputs."""
     Or, Mr, Lr = orc.sdpa(q16, k16, v16)
@@ -232,20 +225,17 @@ def test_config_c3_gqa_prefill(S):
 
 @pytest.mark.parametrize("S,causal", [(2048, False), (1536, True)])
 def test_d256_prefill_long(S, causal):
-    """D = 256 (4-wave workgroups, one per SIMD, three-stage pipelined loop)
-    over many tiles: full-size properties and sampled heads against the fp64
-    oracle, causal included."""
+    """D = 256 over many tiles (the 8-wave wide kernel unmasked, the 4-wave
+    kernel with its three-stage pipelined loop causal): full-size properties
+    and all 16 query heads against the fp64 oracle."""
     B, H_q, H_kv, D = 1, 16, 4, 256
     _announce(test="d256_long", S=S, causal=causal)
     q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, S, S, D, 6000 + S)
     O, Mi, Li = _run_kf(q16, k16, v16, causal=causal)
     _property_checks(O, Mi, Li, v16, H_q, H_kv)
-    for b, h in [(0, 0), (0, 9), (0, 15)]:
-        hk = h // (H_q // H_kv)
-        Or, Mr, Lr = orc.sdpa(q16[b:b + 1, h:h + 1], k16[b:b + 1, hk:hk + 1],
-                              v16[b:b + 1, hk:hk + 1], causal=causal)
-        _check(O[b:b + 1, h:h + 1], Or, f"D=256 S={S} causal={causal} head {h}")
-        _check_stats(Mi[b:b + 1, h:h + 1], Li[b:b + 1, h:h + 1], Mr, Lr, f"D=256 head {h}")
+    Or, Mr, Lr = orc.sdpa(q16, k16, v16, causal=causal)
+    _check(O, Or, f"D=256 S={S} causal={causal}")
+    _check_stats(Mi, Li, Mr, Lr, f"D=256 S={S} causal={causal}")
 
 
 def test_config_c2_gqa_decode():
@@ -264,7 +254,7 @@ def test_config_c4_mqa_d64():
     q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, S, S, D, 4000)
     O, Mi, Li = _run_kf(q16, k16, v16)
     _property_checks(O, Mi, Li, v16, H_q, H_kv)
-    _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (0, 17), (0, 31)])
+    _all_heads_check(O, Mi, Li, q16, k16, v16, "C4a")
     _announce(config="C4b", kv=S)
     q1 = np.ascontiguousarray(q16[:, :, :1])
     O1, M1, L1 = _run_kf(q1, k16, v16)
@@ -289,7 +279,7 @@ def test_long_context_decode(H_q, H_kv, kv, splits):
     """One sequence of 128 K / 256 K keys (GQA and MQA with 32 query rows per
     KV head) on the streaming decode kernel: one 8-wave workgroup per CU, the
     MQA case close to the merge kernel's one-pass capacity of 256 splits;
-    sampled heads against the oracle plus properties."""
+    all 32 query heads against the oracle plus properties."""
     import kernelfoundry_amd as kf
     B, D = 1, 128
     pl = kf.plan(B, 1, kv, H_q, H_kv, D)
@@ -298,7 +288,7 @@ def test_long_context_decode(H_q, H_kv, kv, splits):
     q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 1, kv, D, 9000 + H_kv)
     O, Mi, Li = _run_kf(q16, k16, v16)
     _property_checks(O, Mi, Li, v16, H_q, H_kv)
-    _sampled_heads_check(O, Mi, Li, q16, k16, v16, [(0, 0), (0, H_q - 1)])
+    _all_heads_check(O, Mi, Li, q16, k16, v16, f"long decode H_kv={H_kv} kv={kv}")
 
 
 @pytest.mark.parametrize("B,per_block", [(2, 4), (16, 1)])
