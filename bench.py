@@ -28,6 +28,8 @@ half of the metric):
                      back-to-back dispatch (one kernel boundary), timed the
                      same way; ``decode.graph``: the same steps replayed from
                      one captured HIP graph.
+  * ``decode_b32.floor`` -- beside configs[4]: the same bare read of its
+                     1.07 GB of K/V, the bandwidth a read-only kernel reaches.
   * ``decode_sweep`` -- the reference bench's decode shapes (B=1 KV=512..4096,
                      B=8 KV=512/1024, MQA KV=512/1024; tests/bench_flash_attn.cu:
                      154-159, 181-182), each rotated over > 512 MB of sets,
@@ -607,6 +609,15 @@ def main():
         if args.only:
             return
         results["decode_b32"]["parity"] = parity_spot_check(torch, rb, [(0, 0), (31, 31)])
+        # The bandwidth a kernel that only reads the same 1.07 GB of K and V
+        # reaches on this GPU: the ceiling the decode's roofline fraction is
+        # measured against in practice.
+        read_us, _, read_bytes = decode_floors(torch, load_probe(kf), rb.sets, steps, warmup)
+        results["decode_b32"]["floor"] = {
+            "read_us": round(read_us, 2), "read_gbs": round(read_bytes / (read_us * 1e3), 1),
+            "read_bytes": read_bytes,
+            "decode_vs_read": round(read_us / results["decode_b32"]["latency_us"], 4),
+            "note": "kf_probe_read of the same K and V bytes (16-byte non-temporal loads, no compute)"}
         del rb
 
     if args.only in (None, "decode_paged"):
@@ -705,6 +716,7 @@ def main():
                          "unit": "GB/s", "frac": round(b32["gbs"] / PEAK_HBM_GBS, 4),
                          "bytes_per_launch": b32["bytes"]},
             "path": b32["path"], "splits": b32["splits"],
+            "floor": b32["floor"],
             "parity": b32["parity"],
         },
         "prefill_causal": results["prefill_causal"],
