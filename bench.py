@@ -36,7 +36,8 @@ half of the metric):
                      with the same read floor.
   * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep),
                      the MQA D=64 configs[3] and the configs[2] shape at
-                     D=256 (the reference's largest head dimension).
+                     D=256 (the reference's largest head dimension), plain
+                     and causal (visible-pair FLOPs).
 
 FLOPs = 4*B*H_q*q_len*kv_len*D and bytes = fp16 Q + unique fp16 K,V + fp32 O
 (tests/bench_flash_attn.cu:125-131).  ``roofline.achieved`` divides those by
@@ -529,14 +530,17 @@ def main():
 
     results = {}
 
-    def run_prefill(S, H_kv=8, D=128, steps_=steps, check=None):
+    def run_prefill(S, H_kv=8, D=128, steps_=steps, check=None, causal=False):
         sets = [_inputs(torch, 1, 32, H_kv, S, S, D, 1234 + S)]
-        r = Runner(torch, kf, sets, D)
+        r = Runner(torch, kf, sets, D, flags=kf.KF_ATTN_CAUSAL if causal else 0)
         ms, kern_mean, kern_med = time_steps(torch, r, steps_, warmup)
-        f = flops(1, 32, S, S, D)
+        f = causal_flops(1, 32, S, D) if causal else flops(1, 32, S, S, D)
         out = {"S": S, "H_kv": H_kv, "D": D, "ms": ms, "tflops": f / (ms * 1e9),
                "kernel_ms_mean": kern_mean, "kernel_tflops": f / (kern_mean * 1e9),
                "grid_blocks": r.plan.grid_blocks}
+        if causal:
+            out["causal"] = True
+            out["kernels"] = kf.kernel_names(1, S, S, 32, H_kv, D, causal=True)
         if check:
             out["parity"] = parity_spot_check(torch, r, check)
         return out
@@ -651,6 +655,7 @@ def main():
     sweep = [run_prefill(S) for S in (512, 1024, 2048)]
     sweep.append(run_prefill(2048, H_kv=1, D=64))
     sweep.append(run_prefill(4096, H_kv=8, D=256))
+    sweep.append(run_prefill(4096, H_kv=8, D=256, causal=True))
     # configs[3] decode: 0.54 MB per set, rotated over > 512 MB of distinct
     # sets like configs[1], so each step reads HBM, not the Infinity Cache.
     dq, _ = run_decode(1, 2048, 960, D=64, H_kv=1)

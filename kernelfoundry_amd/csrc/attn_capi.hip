@@ -225,8 +225,9 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
         // kernel (64 rows per wave, 512 per workgroup) when its rounds of
         // workgroups take less time than the 256-row kernel's; one workgroup
         // runs per CU in either kernel, and a wide row costs kWideRowCost of
-        // a 256-row-kernel row.  D = 256: the wide kernel's 8 waves x 32 rows
-        // against 4 waves x 32 rows, by the same rule (kWide256RowCost).
+        // a 256-row-kernel row.  D = 256, masked calls included: the wide
+        // kernels' 8 waves x 32 rows against 4 waves x 32 rows, by the same
+        // rule (kWide256RowCost).
         const bool wide_ok = ((D == 64 || D == 128) && nw == 8 && ks == 1) || (D == 256 && nw == 4);
         if (wide_ok) {
             const int wrows = D >= 256 ? kf::WideCfg<256>::kRows : kf::WideCfg<128>::kRows;
@@ -271,11 +272,15 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
     if (pl.path == KF_PATH_PREFILL) {
         const bool mask = prm.causal || prm.kv_lens;
         if constexpr (D >= 256) {
-            if (!mask && pl.wide_row_tiles > 0) {
+            if (pl.wide_row_tiles > 0) {
                 kf::AttnParams pw = prm;
                 pw.row_tiles = pl.wide_row_tiles;
-                kf::kf_attn_prefill_wide_kernel<D><<<dim3(pl.wide_grid), dim3(kf::WideCfg<D>::kThreads), 0,
-                                                     stream>>>(pw);
+                if (mask)
+                    kf::kf_attn_prefill_wide_kernel<D, true><<<dim3(pl.wide_grid),
+                                                                dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
+                else
+                    kf::kf_attn_prefill_wide_kernel<D, false><<<dim3(pl.wide_grid), dim3(kf::WideCfg<D>::kThreads), 0,
+                                                         stream>>>(pw);
                 return hipGetLastError();
             }
             launch_prefill<D, 4>(pl, prm, mask, stream);
@@ -297,7 +302,7 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
                 if (!mask && pl.wide_row_tiles > 0) {
                     kf::AttnParams pw = prm;
                     pw.row_tiles = pl.wide_row_tiles;
-                    kf::kf_attn_prefill_wide_kernel<D><<<dim3(pl.wide_grid), dim3(kf::WideCfg<D>::kThreads), 0,
+                    kf::kf_attn_prefill_wide_kernel<D, false><<<dim3(pl.wide_grid), dim3(kf::WideCfg<D>::kThreads), 0,
                                                          stream>>>(pw);
                     return hipGetLastError();
                 }
@@ -506,7 +511,7 @@ int describe_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const 
     plan->num_splits = pl.n_splits;
     plan->kv_per_split = pl.kv_per_split;
     // The unmasked dispatch (kf_attn_fwd); masked calls of kf_attn_fwd_ex
-    // run the 256-row kernel's grid.
+    // run the 256-row kernel's grid at D = 64 / 128 and this grid at D = 256.
     plan->grid_blocks = pl.wide_row_tiles > 0 ? pl.wide_grid : pl.grid;
     plan->block_threads = pl.wide_row_tiles > 0 ? kf::WideCfg<128>::kThreads : pl.threads;
     plan->workspace_bytes = pl.ws_bytes;
@@ -538,8 +543,8 @@ int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
     int n;
     if (pl.path == KF_PATH_PREFILL) {
         const bool mask = (flags & KF_ATTN_CAUSAL) || kv_lens;
-        if (!mask && pl.wide_row_tiles > 0)
-            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d>", D);
+        if (pl.wide_row_tiles > 0 && (!mask || D >= 256))
+            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d, %s>", D, mask ? "true" : "false");
         else
             n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_kernel<%d, %s, %d, %d>", D,
                          mask ? "true" : "false", pl.waves, pl.kv_groups);

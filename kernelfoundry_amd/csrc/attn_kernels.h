@@ -1300,7 +1300,11 @@ template <int D> struct WideCfg {
     static constexpr bool kXorOff = D >= 256;
 };
 
-template <int D>
+// kMask: causal masking and/or per-sequence key counts, as in
+// kf_attn_prefill_kernel; built for one row block per wave (D = 256).  (The
+// body sits in the kernel itself: moved into a shared device function, the
+// unmasked kernel compiled to a different, 0.5 % slower schedule.)
+template <int D, bool kMask>
 __global__ __launch_bounds__(WideCfg<D>::kThreads, 2)
 void kf_attn_prefill_wide_kernel(AttnParams p) {
     static_assert(D == 64 || D == 128 || D == 256, "wide prefill: D = 64, 128 or 256");
@@ -1326,18 +1330,62 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     // LDS reads and no K / V read needs address arithmetic (measured +1.6 %).
     __shared__ __attribute__((aligned(256))) char q1_lds[kQ1Lds ? kHalfRows * D * 2 : 16];
 
+    static_assert(!kMask || (D == 256 && kRB == 1 && !kPipe && SR == Cfg::BC),
+                  "masking: D = 256, one row block, one-tile stages");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // Row wave.  Causal: waves w and w + 4 share a SIMD and get row blocks w
+    // and 7 - w, so that the fully masked tiles each wave skips add up to the
+    // same count on every SIMD.
+    const int wave = (kMask && p.causal && wave_id >= 4) ? 11 - wave_id : wave_id;
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x, p.xcds);
-    const int rt = blk % p.row_tiles;
+    int rt = blk % p.row_tiles;
     const int grp = blk / p.row_tiles;
     const int R = p.rows_per_group;
     const int kv_len = p.kv_len;
     const float c = p.scale_log2;
-    const int ntiles = (kv_len + BC - 1) / BC;
-    const int nstages = (kv_len + SR - 1) / SR;
+    // Causal: row tiles longest first on every XCD (as kf_attn_prefill_kernel).
+    if (kMask && p.causal) {
+        const int q_len = p.q_len;
+        if (q_len % kRows == 0) {
+            const int T = q_len / kRows, heads = R / q_len;
+            rt = (rt % heads) * T + (T - 1 - rt / heads);
+        } else {
+            rt = p.row_tiles - 1 - rt;
+        }
+    }
+    // Keys this workgroup needs (blk_lim) and, per wave, the smallest row
+    // limit (below it no masking is needed) and the largest (from it on
+    // every score of the wave is masked).
+    int kvb = kv_len, blk_lim = kv_len, wave_min = kv_len, wave_max = kv_len;
+    if constexpr (kMask) {
+        kvb = batch_kv_len(p, grp);
+        blk_lim = wave_min = wave_max = kvb;
+        if (p.causal) {
+            const int q_len = p.q_len;
+            const int r0 = rt * kRows, r1 = min(R, r0 + kRows) - 1;
+            int lo, hi;
+            qi_range(r0, r1, q_len, lo, hi);
+            blk_lim = row_kv_limit(p, kvb, hi);
+            const int w0 = r0 + wave * 32;
+            if (w0 < R) {
+                qi_range(w0, min(R, w0 + 32) - 1, q_len, lo, hi);
+                wave_min = row_kv_limit(p, kvb, lo);
+                wave_max = row_kv_limit(p, kvb, hi);
+            } else {
+                wave_min = blk_lim;
+                wave_max = 0;
+            }
+        }
+    }
+    const int ntiles = (blk_lim + BC - 1) / BC;
+    const int nstages = (blk_lim + SR - 1) / SR;
+    // Tiles with a key visible to some row of this wave; the later ones are
+    // skipped (their scores would add exactly nothing), the wave still
+    // taking part in the stage barriers and copies.
+    const int nt_w = kMask ? min(ntiles, (wave_max + BC - 1) / BC) : ntiles;
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
     const char* Kh = reinterpret_cast<const char*>(p.K + (size_t)grp * kv_len * D);
@@ -1428,6 +1476,21 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     // row R - 1 and are never stored.
     const int row0 = rt * kRows + wave * 32 + (lane & 31);
     const int row1 = row0 + kHalfRows;
+    if (kMask && ntiles == 0) {
+        // No key for any row of this workgroup (workgroup-uniform).
+        if (row0 < R) {
+            const size_t ri = (size_t)grp * R + row0;
+#pragma unroll
+            for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) store_out4(p, ri * D + 32 * td + 8 * i + 4 * g, f32x4{0.f, 0.f, 0.f, 0.f});
+            if (g == 0) store_stats(p, ri, -INFINITY, 0.f);
+        }
+        return;
+    }
+    // This lane's query row sees keys [0, lim_lane) (padding rows: blk_lim).
+    int lim_lane = kv_len;
+    if constexpr (kMask) lim_lane = row0 < R ? row_kv_limit(p, kvb, row0 % p.q_len) : blk_lim;
 
     issue_stage(buf0, 0);
     f16x8 q0[kNKK], q1[(kRB == 2 && !kQ1Lds) ? kNKK : 1];
@@ -1484,14 +1547,15 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             }
         }
     };
-    // Keys past kv_len in tile t (the last tile) -> -inf.  Register r of
+    // Keys at or past the lane's limit in tile t -> -inf (unmasked: the keys
+    // past kv_len in the last tile).  Register r of
     // lane l holds key 8 (r / 4) + 4 (l / 32) + r % 4 of the tile: compare
     // 8 (r / 4) + r % 4 (an inline constant) with the limit less 4 (l / 32),
     // so no per-register key index stays live across the loop.
     auto tail_mask = [&](f32x16 (&s0)[1], f32x16 (&s1)[1], int t) {
-        if ((t + 1) * BC > kv_len) {
+        if ((t + 1) * BC > wave_min) {
             asm volatile("" ::: "memory");
-            const int lg = kv_len - t * BC - 4 * g;
+            const int lg = lim_lane - t * BC - 4 * g;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 if (8 * (r >> 2) + (r & 3) >= lg) {
@@ -1524,12 +1588,15 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
         // One 32-key tile at `stage`: S^T of both blocks, the row max / lazy
         // rescale / exp2 of each, then P.V for both.
         auto tile = [&](const char* stage, int t) {
+            if (kMask && t >= nt_w) return;  // fully masked for this wave (wave-uniform)
             f32x16 s0[1], s1[1];
             qk2(stage, s0, s1);
             tail_mask(s0, s1, t);
             f16x8 p0[2], p1[2];
             block_update_max<kNTD>(st0, block_rowmax<1>(s0), c, inv_c, o0);
-            block_exp(s0[0], c, -st0.m, p0[0], p0[1], st0.l);
+            // A row that has seen no key yet (masked) keeps m = -inf and must
+            // get P = 0, not NaN.
+            block_exp(s0[0], c, (kMask && st0.m == -INFINITY) ? 0.f : -st0.m, p0[0], p0[1], st0.l);
             if constexpr (kRB == 2) {
                 block_update_max<kNTD>(st1, block_rowmax<1>(s1), c, inv_c, o1);
                 block_exp(s1[0], c, -st1.m, p1[0], p1[1], st1.l);
@@ -1607,12 +1674,15 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
         }
     }
 
-    // ---- Epilogue: both row blocks (every row saw key 0, so l > 0). ----
+    // ---- Epilogue: both row blocks (unmasked, every row saw key 0, so l > 0). ----
     const float l0 = sum_xor32(st0.l);
     if (row0 < R) {
         const size_t ri = (size_t)grp * R + row0;
-        store_o_row_any<D>(p, ri, o0, 1.0f / l0, g);
-        if (g == 0) store_stats(p, ri, st0.rmax * p.scale, l0 * exp2_hw(st0.m - st0.rmax * p.scale_log2));
+        const bool empty = kMask && !(l0 > 0.f);  // masked: no visible key
+        store_o_row_any<D>(p, ri, o0, empty ? 0.f : 1.0f / l0, g);
+        if (g == 0)
+            store_stats(p, ri, st0.rmax * p.scale,
+                        empty ? 0.f : l0 * exp2_hw(st0.m - st0.rmax * p.scale_log2));
     }
     if (kRB == 2 && row1 < R) {
         const float l1 = sum_xor32(st1.l);

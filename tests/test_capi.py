@@ -170,7 +170,7 @@ def test_plans_for_baseline_configs():
     assert p.path == "prefill" and p.rows_per_group == 4 * 4096
     assert p.block_threads == 512                    # 8 waves x 64 query rows
     assert p.grid_blocks == 8 * (4 * 4096 // 512) == 256
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false>"
     # masked: the 256-row kernel (8 waves x 32 rows), 512 workgroups
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == "kf_attn_prefill_kernel<128, true, 8, 1>"
     p = kf.plan(1, 2048, 2048, 32, 8, 128)           # S = 2048: 128 wide workgroups would idle CUs
@@ -264,10 +264,13 @@ def test_prefill_waves_per_workgroup(S, H_kv, D, waves, groups):
     p = kf.plan(1, S, S, 32, H_kv, D)
     wide = kf.kernel_names(1, S, S, 32, H_kv, D).startswith("kf_attn_prefill_wide_kernel")
     assert p.path == "prefill" and p.block_threads == (512 if wide else 64 * waves)
-    # Masked calls always run this kernel; unmasked ones may run the wide
-    # kernel instead (test_wide_prefill_selection).
-    assert kf.kernel_names(1, S, S, 32, H_kv, D, causal=True) == \
-        f"kf_attn_prefill_kernel<{D}, true, {waves}, {groups}>"
+    # Masked calls run this kernel at D = 64 / 128; unmasked ones, and masked
+    # ones at D = 256, may run a wide kernel instead (test_wide_prefill_selection).
+    masked_name = kf.kernel_names(1, S, S, 32, H_kv, D, causal=True)
+    if wide and D == 256:
+        assert masked_name == "kf_attn_prefill_wide_kernel<256, true>"
+    else:
+        assert masked_name == f"kf_attn_prefill_kernel<{D}, true, {waves}, {groups}>"
     rows = 32 * waves // groups
     R = 32 // H_kv * S
     if wide:
@@ -378,7 +381,7 @@ def test_plan_for_cus_rejects_bad_counts(lib):
 def test_kernel_names_follow_the_plan(lib):
     """kf_attn_kernel_names names the kernels in launch order, as the
     profiler lists them."""
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false>"
     assert kf.kernel_names(1, 2048, 2048, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 1>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == \
         "kf_attn_prefill_kernel<128, true, 8, 1>"
@@ -386,8 +389,11 @@ def test_kernel_names_follow_the_plan(lib):
         "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 512, 512, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 4>"
     assert kf.kernel_names(1, 256, 256, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 4, 2>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_wide_kernel<256>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_wide_kernel<256, false>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, causal=True) == "kf_attn_prefill_wide_kernel<256, true>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, masked=True) == "kf_attn_prefill_wide_kernel<256, true>"
     assert kf.kernel_names(1, 2048, 2048, 16, 4, 256) == "kf_attn_prefill_kernel<256, false, 4, 1>"
+    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256, causal=True) == "kf_attn_prefill_kernel<256, true, 4, 1>"
     assert kf.kernel_names(1, 1, 4096, 32, 8, 128) == \
         "kf_attn_decode_short_kernel<128, 1> + kf_attn_split_merge_kernel<128, 8, 4>"
     assert kf.kernel_names(32, 1, 8192, 32, 8, 128) == "kf_attn_decode_kernel<128, false>"

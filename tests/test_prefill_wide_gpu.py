@@ -1,4 +1,4 @@
-"""GPU parity of the wide prefill kernel (kf_attn_prefill_wide_kernel<D>: 8
+"""GPU parity of the wide prefill kernel (kf_attn_prefill_wide_kernel<D, kMask>: 8
 waves x 64 query rows, 512 rows per workgroup, at D = 64 and 128; 8 waves x
 32 rows at D = 256).
 
@@ -18,12 +18,22 @@ The wide kernel computes every row with the same operation order as the
 256-row kernel (the 128-row 4-wave kernel at D = 256), so its output must
 also equal, bit for bit, that kernel's on the same inputs (run through
 kf_attn_fwd_ex with every sequence's key count equal to kv_len, which selects
-that kernel's masked instantiation with no key masked).
+that kernel's masked instantiation with no key masked; at D = 256 the
+masked call runs kf_attn_prefill_wide_kernel<256, true>, whose output with
+no key masked must equal the unmasked wide kernel's bit for bit).
+
+At D = 256 masked calls (causal and/or per-sequence key counts) run
+kf_attn_prefill_wide_kernel<256, true> when the planner chooses the wide
+grid: MASKED_CASES cover causal with q_len = kv_len, kv_len > q_len and
+q_len > kv_len (rows without keys), key counts with an empty sequence, both
+together, and MQA-like GQA ratio 16, against the oracle with rows without
+keys exactly O = 0, Mi = -inf, Li = 0.
 """
 import numpy as np
 import pytest
 
 from oracle import attn_oracle as orc
+from tests._parity import run_and_check
 
 pytestmark = pytest.mark.gpu
 
@@ -68,7 +78,7 @@ def test_wide_prefill_matches_oracle(case):
     B, H_q, H_kv, q_len, kv_len, D = case
     names = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D)
     print("case", case, names, flush=True)
-    assert names == f"kf_attn_prefill_wide_kernel<{D}>", names
+    assert names == f"kf_attn_prefill_wide_kernel<{D}, false>", names
     (q16, k16, v16), (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 11 + kv_len)
     O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True)
     torch.cuda.synchronize()
@@ -89,8 +99,10 @@ def test_wide_prefill_equals_256_row_kernel_bitwise(case):
     B, H_q, H_kv, q_len, kv_len, D = case
     masked = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, masked=True)
     print("case", case, masked, flush=True)
-    waves = 4 if D == 256 else 8
-    assert masked == f"kf_attn_prefill_kernel<{D}, true, {waves}, 1>", masked
+    if D == 256:  # masked D = 256 calls run the masked wide kernel on this grid
+        assert masked == "kf_attn_prefill_wide_kernel<256, true>", masked
+    else:
+        assert masked == f"kf_attn_prefill_kernel<{D}, true, 8, 1>", masked
     _, (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 5)
     full = torch.full((B,), kv_len, dtype=torch.int32, device="cuda")
     Ow, Mw, Lw = kf.attn_fwd(Q, K, V, return_stats=True)
@@ -98,3 +110,28 @@ def test_wide_prefill_equals_256_row_kernel_bitwise(case):
     torch.cuda.synchronize()
     assert torch.equal(Ow, On), f"O differs: max {(Ow - On).abs().max().item():.3g}"
     assert torch.equal(Mw, Mn) and torch.equal(Lw, Ln), "Mi / Li differ"
+
+
+MASKED_CASES = [
+    # B, H_q, H_kv, q_len, kv_len, causal, kv_lens        what it hits
+    (4, 16, 4, 600, 600, True, None),                      # causal, ragged row tiles
+    (4, 16, 4, 600, 777, True, None),                      # causal, kv_len > q_len
+    (4, 16, 4, 700, 500, True, None),                      # causal, 200 rows without keys
+    (4, 16, 4, 600, 777, False, [777, 0, 31, 500]),        # key counts, an empty sequence
+    (4, 16, 4, 640, 700, True, [700, 129, 0, 640]),        # causal + key counts
+    (4, 32, 2, 300, 300, True, None),                      # GQA ratio 16, causal
+]
+
+
+def _mids(c):
+    return "B{}_Hq{}_Hkv{}_q{}_kv{}_c{}_{}".format(*c[:5], int(c[5]), "lens" if c[6] is not None else "full")
+
+
+@pytest.mark.parametrize("case", MASKED_CASES, ids=_mids)
+def test_wide_masked_prefill_d256_matches_oracle(case):
+    import kernelfoundry_amd as kf
+    B, H_q, H_kv, q_len, kv_len, causal, kv_lens = case
+    name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, 256, causal=causal, masked=kv_lens is not None)
+    print("case", case, name, flush=True)
+    assert name == "kf_attn_prefill_wide_kernel<256, true>", name
+    run_and_check(B, H_q, H_kv, q_len, kv_len, 256, causal, kv_lens, 300 + q_len)

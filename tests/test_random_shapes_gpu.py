@@ -75,12 +75,13 @@ def _layout(kf, B, H_q, H_kv, q_len, kv_len, D, causal=False, masked=False):
     """(path, kernel) for decode, kernel "short32" / "short64" (one wave per
     split of that many keys) or "stream"; ("prefill", waves, kv_groups) for
     prefill, read from the kernel name (kf_attn_prefill_kernel<D, mask,
-    waves, kv_groups>), or ("prefill", "wide") for kf_attn_prefill_wide_kernel."""
+    waves, kv_groups>), or ("prefill", "wide") for kf_attn_prefill_wide_kernel
+    with either mask flag."""
     p = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
     if p.path != "prefill":
         return (p.path, f"short{p.kv_per_split}" if p.splits_per_block == 4 else "stream")
     name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, causal=causal, masked=masked)
-    if name.startswith("kf_attn_prefill_wide_kernel"):
+    if name.startswith("kf_attn_prefill_wide"):  # the wide kernel, masked or not
         return ("prefill", "wide")
     waves, groups = (int(x) for x in name.rstrip(">").split(",")[-2:])
     return ("prefill", waves, groups)
