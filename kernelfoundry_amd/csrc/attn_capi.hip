@@ -225,9 +225,10 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
         // kernel (64 rows per wave, 512 per workgroup) when its rounds of
         // workgroups take less time than the 256-row kernel's; one workgroup
         // runs per CU in either kernel, and a wide row costs kWideRowCost of
-        // a 256-row-kernel row.  D = 256, masked calls included: the wide
-        // kernels' 8 waves x 32 rows against 4 waves x 32 rows, by the same
-        // rule (kWide256RowCost).
+        // a 256-row-kernel row (also for calls with key counts; causal ones
+        // keep the 256-row kernel).  D = 256, masked calls included: the
+        // wide kernels' 8 waves x 32 rows against 4 waves x 32 rows, by the
+        // same rule (kWide256RowCost).
         const bool wide_ok = ((D == 64 || D == 128) && nw == 8 && ks == 1) || (D == 256 && nw == 4);
         if (wide_ok) {
             const int wrows = D >= 256 ? kf::WideCfg<256>::kRows : kf::WideCfg<128>::kRows;
@@ -299,11 +300,17 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
                 }
             }
             if constexpr (D == 64 || D == 128) {
-                if (!mask && pl.wide_row_tiles > 0) {
+                // Two row blocks per wave: key counts give both one limit, so
+                // only causal calls stay on the 256-row kernel.
+                if (!prm.causal && pl.wide_row_tiles > 0) {
                     kf::AttnParams pw = prm;
                     pw.row_tiles = pl.wide_row_tiles;
-                    kf::kf_attn_prefill_wide_kernel<D, false><<<dim3(pl.wide_grid), dim3(kf::WideCfg<D>::kThreads), 0,
-                                                         stream>>>(pw);
+                    if (mask)
+                        kf::kf_attn_prefill_wide_kernel<D, true><<<dim3(pl.wide_grid),
+                                                                   dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
+                    else
+                        kf::kf_attn_prefill_wide_kernel<D, false><<<dim3(pl.wide_grid),
+                                                                    dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
                     return hipGetLastError();
                 }
             }
@@ -510,7 +517,7 @@ int describe_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const 
     plan->rows_per_group = pl.R;
     plan->num_splits = pl.n_splits;
     plan->kv_per_split = pl.kv_per_split;
-    // The unmasked dispatch (kf_attn_fwd); masked calls of kf_attn_fwd_ex
+    // The unmasked dispatch (kf_attn_fwd); causal calls of kf_attn_fwd_ex
     // run the 256-row kernel's grid at D = 64 / 128 and this grid at D = 256.
     plan->grid_blocks = pl.wide_row_tiles > 0 ? pl.wide_grid : pl.grid;
     plan->block_threads = pl.wide_row_tiles > 0 ? kf::WideCfg<128>::kThreads : pl.threads;
@@ -542,8 +549,9 @@ int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
     char tmp[192];
     int n;
     if (pl.path == KF_PATH_PREFILL) {
-        const bool mask = (flags & KF_ATTN_CAUSAL) || kv_lens;
-        if (pl.wide_row_tiles > 0 && (!mask || D >= 256))
+        const bool causal = (flags & KF_ATTN_CAUSAL) != 0;
+        const bool mask = causal || kv_lens;
+        if (pl.wide_row_tiles > 0 && (!causal || D >= 256))
             n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d, %s>", D, mask ? "true" : "false");
         else
             n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_kernel<%d, %s, %d, %d>", D,

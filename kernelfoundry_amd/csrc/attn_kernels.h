@@ -1301,9 +1301,11 @@ template <int D> struct WideCfg {
 };
 
 // kMask: causal masking and/or per-sequence key counts, as in
-// kf_attn_prefill_kernel; built for one row block per wave (D = 256).  (The
-// body sits in the kernel itself: moved into a shared device function, the
-// unmasked kernel compiled to a different, 0.5 % slower schedule.)
+// kf_attn_prefill_kernel.  Causal masking needs one row block per wave
+// (D = 256); with two (D = 64 / 128) the host launches the masked kernel
+// for key counts only, which give every row of a sequence the same limit.
+// (The body sits in the kernel itself: moved into a shared device function,
+// the unmasked kernel compiled to a different, 0.5 % slower schedule.)
 template <int D, bool kMask>
 __global__ __launch_bounds__(WideCfg<D>::kThreads, 2)
 void kf_attn_prefill_wide_kernel(AttnParams p) {
@@ -1330,15 +1332,15 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     // LDS reads and no K / V read needs address arithmetic (measured +1.6 %).
     __shared__ __attribute__((aligned(256))) char q1_lds[kQ1Lds ? kHalfRows * D * 2 : 16];
 
-    static_assert(!kMask || (D == 256 && kRB == 1 && !kPipe && SR == Cfg::BC),
-                  "masking: D = 256, one row block, one-tile stages");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
     // Row wave.  Causal: waves w and w + 4 share a SIMD and get row blocks w
     // and 7 - w, so that the fully masked tiles each wave skips add up to the
     // same count on every SIMD.
-    const int wave = (kMask && p.causal && wave_id >= 4) ? 11 - wave_id : wave_id;
+    // Causal masking is compiled in for one row block per wave only.
+    const bool causal = kMask && kRB == 1 && p.causal;
+    const int wave = (causal && wave_id >= 4) ? 11 - wave_id : wave_id;
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x, p.xcds);
     int rt = blk % p.row_tiles;
@@ -1347,7 +1349,7 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     const int kv_len = p.kv_len;
     const float c = p.scale_log2;
     // Causal: row tiles longest first on every XCD (as kf_attn_prefill_kernel).
-    if (kMask && p.causal) {
+    if (causal) {
         const int q_len = p.q_len;
         if (q_len % kRows == 0) {
             const int T = q_len / kRows, heads = R / q_len;
@@ -1363,7 +1365,7 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     if constexpr (kMask) {
         kvb = batch_kv_len(p, grp);
         blk_lim = wave_min = wave_max = kvb;
-        if (p.causal) {
+        if (causal) {
             const int q_len = p.q_len;
             const int r0 = rt * kRows, r1 = min(R, r0 + kRows) - 1;
             int lo, hi;
@@ -1478,19 +1480,24 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     const int row1 = row0 + kHalfRows;
     if (kMask && ntiles == 0) {
         // No key for any row of this workgroup (workgroup-uniform).
-        if (row0 < R) {
-            const size_t ri = (size_t)grp * R + row0;
 #pragma unroll
-            for (int td = 0; td < kNTD; ++td)
+        for (int b = 0; b < kRB; ++b) {
+            const int row = b == 0 ? row0 : row1;
+            if (row < R) {
+                const size_t ri = (size_t)grp * R + row;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) store_out4(p, ri * D + 32 * td + 8 * i + 4 * g, f32x4{0.f, 0.f, 0.f, 0.f});
-            if (g == 0) store_stats(p, ri, -INFINITY, 0.f);
+                for (int td = 0; td < kNTD; ++td)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        store_out4(p, ri * D + 32 * td + 8 * i + 4 * g, f32x4{0.f, 0.f, 0.f, 0.f});
+                if (g == 0) store_stats(p, ri, -INFINITY, 0.f);
+            }
         }
         return;
     }
     // This lane's query row sees keys [0, lim_lane) (padding rows: blk_lim).
     int lim_lane = kv_len;
-    if constexpr (kMask) lim_lane = row0 < R ? row_kv_limit(p, kvb, row0 % p.q_len) : blk_lim;
+    if constexpr (kMask) lim_lane = !causal ? kvb : row0 < R ? row_kv_limit(p, kvb, row0 % p.q_len) : blk_lim;
 
     issue_stage(buf0, 0);
     f16x8 q0[kNKK], q1[(kRB == 2 && !kQ1Lds) ? kNKK : 1];

@@ -382,10 +382,10 @@ def test_kernel_names_follow_the_plan(lib):
     """kf_attn_kernel_names names the kernels in launch order, as the
     profiler lists them."""
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, masked=True) == "kf_attn_prefill_wide_kernel<128, true>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 2048, 2048, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 1>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == \
-        "kf_attn_prefill_kernel<128, true, 8, 1>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, masked=True) == \
         "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 512, 512, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 4>"
     assert kf.kernel_names(1, 256, 256, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 4, 2>"

@@ -16,18 +16,19 @@ to the north-star bar (max |got - ref| <= 2e-3, ||got - ref|| / ||ref|| <=
 
 The wide kernel computes every row with the same operation order as the
 256-row kernel (the 128-row 4-wave kernel at D = 256), so its output must
-also equal, bit for bit, that kernel's on the same inputs (run through
-kf_attn_fwd_ex with every sequence's key count equal to kv_len, which selects
-that kernel's masked instantiation with no key masked; at D = 256 the
-masked call runs kf_attn_prefill_wide_kernel<256, true>, whose output with
-no key masked must equal the unmasked wide kernel's bit for bit).
+equal, bit for bit, that kernel's on the same inputs (PAIRS, below), and
+the masked wide kernel with every sequence's key count equal to kv_len must
+give the unmasked one's bits.
 
-At D = 256 masked calls (causal and/or per-sequence key counts) run
-kf_attn_prefill_wide_kernel<256, true> when the planner chooses the wide
-grid: MASKED_CASES cover causal with q_len = kv_len, kv_len > q_len and
-q_len > kv_len (rows without keys), key counts with an empty sequence, both
-together, and MQA-like GQA ratio 16, against the oracle with rows without
-keys exactly O = 0, Mi = -inf, Li = 0.
+Masked calls run kf_attn_prefill_wide_kernel<D, true> when the planner
+chooses the wide grid: at D = 256 causal and/or per-sequence key counts, at
+D = 64 / 128 key counts only (causal calls keep the 256-row kernel).
+MASKED_CASES cover causal with q_len = kv_len, kv_len > q_len and q_len >
+kv_len (rows without keys), key counts with an empty sequence and a single
+key, both together, and GQA ratio 16, against the oracle with rows without
+keys exactly O = 0, Mi = -inf, Li = 0.  PAIRS check the wide kernels
+against the 32-row kernel bit for bit through the planner's own choice
+(B = 1 plans the 32-row kernel, B = 2 the wide one, at the same shape).
 """
 import numpy as np
 import pytest
@@ -93,16 +94,13 @@ def test_wide_prefill_matches_oracle(case):
 
 @pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[4], CASES[6], CASES[8], CASES[10]],
                          ids=_ids)
-def test_wide_prefill_equals_256_row_kernel_bitwise(case):
+def test_wide_masked_without_masking_equals_unmasked_bitwise(case):
     import kernelfoundry_amd as kf
     torch = _torch()
     B, H_q, H_kv, q_len, kv_len, D = case
     masked = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, masked=True)
     print("case", case, masked, flush=True)
-    if D == 256:  # masked D = 256 calls run the masked wide kernel on this grid
-        assert masked == "kf_attn_prefill_wide_kernel<256, true>", masked
-    else:
-        assert masked == f"kf_attn_prefill_kernel<{D}, true, 8, 1>", masked
+    assert masked == f"kf_attn_prefill_wide_kernel<{D}, true>", masked
     _, (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 5)
     full = torch.full((B,), kv_len, dtype=torch.int32, device="cuda")
     Ow, Mw, Lw = kf.attn_fwd(Q, K, V, return_stats=True)
@@ -113,25 +111,66 @@ def test_wide_prefill_equals_256_row_kernel_bitwise(case):
 
 
 MASKED_CASES = [
-    # B, H_q, H_kv, q_len, kv_len, causal, kv_lens        what it hits
-    (4, 16, 4, 600, 600, True, None),                      # causal, ragged row tiles
-    (4, 16, 4, 600, 777, True, None),                      # causal, kv_len > q_len
-    (4, 16, 4, 700, 500, True, None),                      # causal, 200 rows without keys
-    (4, 16, 4, 600, 777, False, [777, 0, 31, 500]),        # key counts, an empty sequence
-    (4, 16, 4, 640, 700, True, [700, 129, 0, 640]),        # causal + key counts
-    (4, 32, 2, 300, 300, True, None),                      # GQA ratio 16, causal
+    # B, H_q, H_kv, q_len, kv_len, causal, kv_lens, D         what it hits
+    (4, 16, 4, 600, 600, True, None, 256),                     # causal, ragged row tiles
+    (4, 16, 4, 600, 777, True, None, 256),                     # causal, kv_len > q_len
+    (4, 16, 4, 700, 500, True, None, 256),                     # causal, 200 rows without keys
+    (4, 16, 4, 600, 777, False, [777, 0, 31, 500], 256),       # key counts, an empty sequence
+    (4, 16, 4, 640, 700, True, [700, 129, 0, 640], 256),       # causal + key counts
+    (4, 32, 2, 300, 300, True, None, 256),                     # GQA ratio 16, causal
+    (4, 32, 8, 600, 777, False, [777, 0, 31, 500], 128),       # two row blocks per wave: key counts
+    (4, 32, 8, 600, 777, False, [1, 777, 64, 65], 64),         # D = 64 (pipelined loop), key counts
 ]
 
 
 def _mids(c):
-    return "B{}_Hq{}_Hkv{}_q{}_kv{}_c{}_{}".format(*c[:5], int(c[5]), "lens" if c[6] is not None else "full")
+    return "B{}_Hq{}_Hkv{}_q{}_kv{}_c{}_{}_D{}".format(*c[:5], int(c[5]), "lens" if c[6] is not None else "full",
+                                                     c[7])
 
 
 @pytest.mark.parametrize("case", MASKED_CASES, ids=_mids)
-def test_wide_masked_prefill_d256_matches_oracle(case):
+def test_wide_masked_prefill_matches_oracle(case):
     import kernelfoundry_amd as kf
-    B, H_q, H_kv, q_len, kv_len, causal, kv_lens = case
-    name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, 256, causal=causal, masked=kv_lens is not None)
+    B, H_q, H_kv, q_len, kv_len, causal, kv_lens, D = case
+    name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, causal=causal, masked=kv_lens is not None)
     print("case", case, name, flush=True)
-    assert name == "kf_attn_prefill_wide_kernel<256, true>", name
-    run_and_check(B, H_q, H_kv, q_len, kv_len, 256, causal, kv_lens, 300 + q_len)
+    assert name == f"kf_attn_prefill_wide_kernel<{D}, true>", name
+    run_and_check(B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens, 300 + q_len)
+
+
+# At S = 2048 the planner runs the 256-row kernel (the 128-row one at
+# D = 256) for B = 1 and the wide kernel for B = 2: batch 0 of the B = 2 call
+# holds the B = 1 call's inputs, so its O, Mi and Li must be the same bits.
+PAIRS = [
+    # D, H_q, H_kv, causal, batch-0 key count (None: unmasked)
+    (128, 32, 8, False, None),
+    (128, 32, 8, False, 1500),
+    (64, 32, 8, False, None),
+    (64, 32, 8, False, 777),
+    (256, 16, 4, False, None),
+    (256, 16, 4, False, 1111),
+    (256, 16, 4, True, None),
+]
+
+
+@pytest.mark.parametrize("case", PAIRS, ids=lambda c: "D{}_Hq{}_Hkv{}_c{}_{}".format(
+    c[0], c[1], c[2], int(c[3]), "full" if c[4] is None else f"k{c[4]}"))
+def test_wide_and_narrow_kernels_agree_bitwise(case):
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    D, H_q, H_kv, causal, k0 = case
+    S = 2048
+    masked = k0 is not None
+    n1 = kf.kernel_names(1, S, S, H_q, H_kv, D, causal=causal, masked=masked)
+    n2 = kf.kernel_names(2, S, S, H_q, H_kv, D, causal=causal, masked=masked)
+    print("case", case, n1, "|", n2, flush=True)
+    assert n1.startswith("kf_attn_prefill_kernel<") and n2.startswith("kf_attn_prefill_wide_kernel<"), (n1, n2)
+    _, (Q, K, V) = _inputs(2, H_q, H_kv, S, S, D, 77)
+    l1 = torch.tensor([k0], dtype=torch.int32, device="cuda") if masked else None
+    l2 = torch.tensor([k0, S - 5], dtype=torch.int32, device="cuda") if masked else None
+    O1, M1, L1 = kf.attn_fwd(Q[:1].contiguous(), K[:1].contiguous(), V[:1].contiguous(), return_stats=True,
+                             causal=causal, kv_lens=l1)
+    O2, M2, L2 = kf.attn_fwd(Q, K, V, return_stats=True, causal=causal, kv_lens=l2)
+    torch.cuda.synchronize()
+    assert torch.equal(O1[0], O2[0]), f"O differs: max {(O1[0] - O2[0]).abs().max().item():.3g}"
+    assert torch.equal(M1[0], M2[0]) and torch.equal(L1[0], L2[0]), "Mi / Li differ"
