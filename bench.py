@@ -37,7 +37,8 @@ half of the metric):
   * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep),
                      the MQA D=64 configs[3] and the configs[2] shape at
                      D=256 (the reference's largest head dimension), plain
-                     and causal (visible-pair FLOPs).
+                     and causal (visible-pair FLOPs), and configs[2] with a
+                     per-sequence key count of 4000 (FLOPs over those keys).
 
 FLOPs = 4*B*H_q*q_len*kv_len*D and bytes = fp16 Q + unique fp16 K,V + fp32 O
 (tests/bench_flash_attn.cu:125-131).  ``roofline.achieved`` divides those by
@@ -146,9 +147,11 @@ def _inputs(torch, B, H_q, H_kv, q, kv, D, seed):
 class Runner:
     """Pre-resolved kf_attn_fwd call (no allocation inside the timed loop)."""
 
-    def __init__(self, torch, kf, sets, D, flags=0):
+    def __init__(self, torch, kf, sets, D, flags=0, kv_lens=None):
         self.torch, self.kf = torch, kf
         self.flags = flags
+        # Per-sequence key counts (device int32 [B]) for kf_attn_fwd_ex, or None.
+        self.kv_lens = kv_lens
         Q, K, V = sets[0]
         B, H_q, q, _ = Q.shape
         _, H_kv, kv, _ = K.shape
@@ -168,10 +171,11 @@ class Runner:
         Q, K, V = self.sets[j]
         B, q, kv, H_q, H_kv, D = self.shape
         cs = (stream or self.stream).cuda_stream
-        if self.flags:
+        if self.flags or self.kv_lens is not None:
+            lens = None if self.kv_lens is None else self.kv_lens.data_ptr()
             st = self.lib.kf_attn_fwd_ex(Q.data_ptr(), K.data_ptr(), V.data_ptr(),
                                          self.outs[j].data_ptr(), None, None, B, q, kv, H_q, H_kv,
-                                         D, None, self.flags,
+                                         D, lens, self.flags,
                                          self.ws.data_ptr() if self.ws_bytes else None,
                                          self.ws_bytes, cs)
         else:
@@ -530,17 +534,24 @@ def main():
 
     results = {}
 
-    def run_prefill(S, H_kv=8, D=128, steps_=steps, check=None, causal=False):
+    def run_prefill(S, H_kv=8, D=128, steps_=steps, check=None, causal=False, key_count=None):
         sets = [_inputs(torch, 1, 32, H_kv, S, S, D, 1234 + S)]
-        r = Runner(torch, kf, sets, D, flags=kf.KF_ATTN_CAUSAL if causal else 0)
+        lens = None if key_count is None else torch.full((1,), key_count, dtype=torch.int32, device="cuda")
+        r = Runner(torch, kf, sets, D, flags=kf.KF_ATTN_CAUSAL if causal else 0, kv_lens=lens)
         ms, kern_mean, kern_med = time_steps(torch, r, steps_, warmup)
-        f = causal_flops(1, 32, S, D) if causal else flops(1, 32, S, S, D)
+        if causal:
+            f = causal_flops(1, 32, S, D)
+        else:
+            f = flops(1, 32, S, S if key_count is None else key_count, D)
         out = {"S": S, "H_kv": H_kv, "D": D, "ms": ms, "tflops": f / (ms * 1e9),
                "kernel_ms_mean": kern_mean, "kernel_tflops": f / (kern_mean * 1e9),
                "grid_blocks": r.plan.grid_blocks}
         if causal:
             out["causal"] = True
-            out["kernels"] = kf.kernel_names(1, S, S, 32, H_kv, D, causal=True)
+        if key_count is not None:
+            out["key_count"] = key_count
+        if causal or key_count is not None:
+            out["kernels"] = kf.kernel_names(1, S, S, 32, H_kv, D, causal=causal, masked=key_count is not None)
         if check:
             out["parity"] = parity_spot_check(torch, r, check)
         return out
@@ -656,6 +667,9 @@ def main():
     sweep.append(run_prefill(2048, H_kv=1, D=64))
     sweep.append(run_prefill(4096, H_kv=8, D=256))
     sweep.append(run_prefill(4096, H_kv=8, D=256, causal=True))
+    # configs[2] with a per-sequence key count (kf_attn_fwd_ex kv_lens): the
+    # sequence uses its first 4000 of the 4096 allocated key rows.
+    sweep.append(run_prefill(4096, key_count=4000))
     # configs[3] decode: 0.54 MB per set, rotated over > 512 MB of distinct
     # sets like configs[1], so each step reads HBM, not the Infinity Cache.
     dq, _ = run_decode(1, 2048, 960, D=64, H_kv=1)
