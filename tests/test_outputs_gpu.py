@@ -9,7 +9,7 @@ the bits are the references).  LSE must equal Mi + ln(Li) of the fp32 call
 Mi + ln(Li) to 1e-3; rows without keys give LSE = -inf.
 
 Every kernel path that writes O is covered: prefill (unmasked and masked, the
-256-row and the wide 512-row kernel),
+256-row and the wide kernel, masked by key counts and, at D = 256, causal),
 decode without split (O written by the decode kernel), decode with split
 (O written by the merge kernel), and paged decode.
 """
@@ -42,6 +42,8 @@ CASES = [
     (32, 32, 8, 100, 77, 128, False, None),               # wide prefill (512-row workgroups)
     (2, 8, 2, 200, 260, 64, True, [260, 0]),              # prefill, masked, empty sequence
     (1, 4, 4, 64, 64, 256, False, None),                  # prefill D=256
+    (4, 32, 8, 600, 777, 128, False, [777, 0, 31, 500]),  # wide prefill with key counts
+    (4, 16, 4, 700, 500, 256, True, None),                # wide prefill D=256, causal, rows without keys
     (2, 8, 8, 1, 100, 16, False, None),                   # decode, one split
     (2, 32, 8, 1, 3000, 128, True, [3000, 7]),            # decode + merge kernel
 ]
