@@ -7,7 +7,7 @@ the last V row exactly, while every other V row holds -1; Mi must be that
 score and Li exactly 1.  A wrapped or truncated offset would read another
 row and show up as -1 / a wrong Mi.  Run through the decode kernels, the
 small-grid prefill and (65792 / 32896 query rows) the wide prefill kernel
-at D = 128 and 256."""
+at D = 128 and 256, unmasked and masked (key count = kv_len)."""
 import math
 
 import pytest
@@ -25,8 +25,12 @@ def test_last_key_at_the_offset_limit(q_len, H_q, D):
     names = kf.kernel_names(1, q_len, kv, H_q, 1, D)
     print("case", dict(q_len=q_len, H_q=H_q, D=D, kv=kv, path=kf.plan(1, q_len, kv, H_q, 1, D).path,
                        kernels=names), flush=True)
-    if q_len > 1000:  # 65792 / 32896 rows: the wide prefill kernel
+    wide = q_len > 1000  # 65792 / 32896 rows: the wide prefill kernel
+    if wide:
         assert names.startswith("kf_attn_prefill_wide_kernel"), names
+        # ... and its masked instantiation, with the key count set to kv_len
+        masked = kf.kernel_names(1, q_len, kv, H_q, 1, D, masked=True)
+        assert masked == f"kf_attn_prefill_wide_kernel<{D}, true>", masked
     dev = torch.device("cuda")
     K = torch.zeros((1, 1, kv, D), dtype=torch.float16, device=dev)
     V = torch.full((1, 1, kv, D), -1.0, dtype=torch.float16, device=dev)
@@ -35,13 +39,16 @@ def test_last_key_at_the_offset_limit(q_len, H_q, D):
     V[0, 0, -1] = vlast
     Q = torch.full((1, H_q, q_len, D), 0.5, dtype=torch.float16, device=dev)
     try:
-        O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True)
-        torch.cuda.synchronize()
-        want = vlast.float().expand(1, H_q, q_len, D)
-        assert torch.equal(O, want), (O - want).abs().max().item()
-        score = 0.5 * 16.0 * D / math.sqrt(D)      # q.k / sqrt(D)
-        assert torch.allclose(Mi, torch.full_like(Mi, score), rtol=1e-6, atol=1e-4)
-        assert torch.equal(Li, torch.ones_like(Li))
+        runs = [None] + ([torch.tensor([kv], dtype=torch.int32, device=dev)] if wide else [])
+        for lens in runs:
+            O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True, kv_lens=lens)
+            torch.cuda.synchronize()
+            want = vlast.float().expand(1, H_q, q_len, D)
+            assert torch.equal(O, want), (lens is not None, (O - want).abs().max().item())
+            score = 0.5 * 16.0 * D / math.sqrt(D)      # q.k / sqrt(D)
+            assert torch.allclose(Mi, torch.full_like(Mi, score), rtol=1e-6, atol=1e-4)
+            assert torch.equal(Li, torch.ones_like(Li))
+            del O, Mi, Li
     finally:
         del K, V
         torch.cuda.empty_cache()
