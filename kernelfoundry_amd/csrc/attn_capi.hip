@@ -62,6 +62,12 @@ constexpr double kWideRowCost = 0.94;
 // The same for the 8-wave D = 256 kernel (256 rows per workgroup) against the
 // 4-wave one (128 rows): 487 vs 689 us at S = 4096, 32 / 8 heads.
 constexpr double kWide256RowCost = 0.7;
+// D = 256 grids that the 256-row wide kernel does not take run as the wide
+// kernel with two KV groups (8 waves on the 4-wave kernel's 128-row tiles)
+// from this many keys per row on: 78.8 vs 94.0 us at S = 2048, 16 / 4 heads,
+// 25.5 vs 30.7 at S = 512, 32 / 8.  Where the 256-row kernel is taken it
+// stays ahead (S = 1536-5120, 32 / 8 heads: the KV groups 1-6 % slower).
+constexpr int kWide256GroupKeys = 2 * kMinGroupKeys;
 constexpr size_t kWsAlign = 256;
 
 thread_local int g_last_hip_error = 0;
@@ -112,9 +118,11 @@ struct Plan {
     int threads;
     int waves;          // prefill: waves per workgroup
     int kv_groups;      // prefill: KV groups per workgroup (1, 2 or 4)
-    int wide_row_tiles; // prefill without masking: 512-row tiles of the wide
-                        // kernel per KV head, 0 = the 32-row-per-wave kernel
+    int wide_row_tiles; // prefill: row tiles of the wide kernel per KV head (512 rows
+                        // at D = 64 / 128, 256 or, with KV groups, 128 at D = 256),
+                        // 0 = the 32-row-per-wave kernel
     int wide_grid;      // workgroups of the wide kernel
+    int wide_kv_groups; // KV groups of the wide kernel (2: D = 256, 128 rows per workgroup)
     int short_stages;   // decode: 32-key stages per split of the short-split kernel, 0 = streaming kernel
     int merge_cw;       // split merge: float4 columns per wave
     int merge_per;      // split merge: splits per lane
@@ -228,7 +236,8 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
         // a 256-row-kernel row (also for calls with key counts; causal ones
         // keep the 256-row kernel).  D = 256, masked calls included: the
         // wide kernels' 8 waves x 32 rows against 4 waves x 32 rows, by the
-        // same rule (kWide256RowCost).
+        // same rule (kWide256RowCost), else, from kWide256GroupKeys keys on,
+        // the wide kernel with two KV groups on the 4-wave kernel's tiles.
         const bool wide_ok = ((D == 64 || D == 128) && nw == 8 && ks == 1) || (D == 256 && nw == 4);
         if (wide_ok) {
             const int wrows = D >= 256 ? kf::WideCfg<256>::kRows : kf::WideCfg<128>::kRows;
@@ -239,6 +248,11 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
             if (wg <= INT_MAX && (double)rounds_w * wrows * wcost < (double)rounds_n * rows) {
                 p.wide_row_tiles = (int)wrt;
                 p.wide_grid = (int)wg;
+                p.wide_kv_groups = 1;
+            } else if (D == 256 && kv_len >= kWide256GroupKeys) {
+                p.wide_row_tiles = p.row_tiles;  // 128 rows per workgroup
+                p.wide_grid = p.grid;
+                p.wide_kv_groups = 2;
             }
         }
     }
@@ -276,12 +290,17 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
             if (pl.wide_row_tiles > 0) {
                 kf::AttnParams pw = prm;
                 pw.row_tiles = pl.wide_row_tiles;
-                if (mask)
-                    kf::kf_attn_prefill_wide_kernel<D, true><<<dim3(pl.wide_grid),
-                                                                dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
-                else
-                    kf::kf_attn_prefill_wide_kernel<D, false><<<dim3(pl.wide_grid), dim3(kf::WideCfg<D>::kThreads), 0,
-                                                         stream>>>(pw);
+                const dim3 grid(pl.wide_grid), block(kf::WideCfg<D>::kThreads);
+                if (pl.wide_kv_groups == 2) {
+                    if (mask)
+                        kf::kf_attn_prefill_wide_kernel<D, true, 2><<<grid, block, 0, stream>>>(pw);
+                    else
+                        kf::kf_attn_prefill_wide_kernel<D, false, 2><<<grid, block, 0, stream>>>(pw);
+                } else if (mask) {
+                    kf::kf_attn_prefill_wide_kernel<D, true, 1><<<grid, block, 0, stream>>>(pw);
+                } else {
+                    kf::kf_attn_prefill_wide_kernel<D, false, 1><<<grid, block, 0, stream>>>(pw);
+                }
                 return hipGetLastError();
             }
             launch_prefill<D, 4>(pl, prm, mask, stream);
@@ -306,11 +325,11 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
                     kf::AttnParams pw = prm;
                     pw.row_tiles = pl.wide_row_tiles;
                     if (mask)
-                        kf::kf_attn_prefill_wide_kernel<D, true><<<dim3(pl.wide_grid),
-                                                                   dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
+                        kf::kf_attn_prefill_wide_kernel<D, true, 1><<<dim3(pl.wide_grid),
+                                                                      dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
                     else
-                        kf::kf_attn_prefill_wide_kernel<D, false><<<dim3(pl.wide_grid),
-                                                                    dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
+                        kf::kf_attn_prefill_wide_kernel<D, false, 1><<<dim3(pl.wide_grid),
+                                                                       dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
                     return hipGetLastError();
                 }
             }
@@ -552,7 +571,8 @@ int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
         const bool causal = (flags & KF_ATTN_CAUSAL) != 0;
         const bool mask = causal || kv_lens;
         if (pl.wide_row_tiles > 0 && (!causal || D >= 256))
-            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d, %s>", D, mask ? "true" : "false");
+            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d, %s, %d>", D, mask ? "true" : "false",
+                         pl.wide_kv_groups);
         else
             n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_kernel<%d, %s, %d, %d>", D,
                          mask ? "true" : "false", pl.waves, pl.kv_groups);

@@ -760,6 +760,85 @@ __device__ __forceinline__ void block_update_max(RowState& st, float mx, float s
     }
 }
 
+// KV-group merge (KS > 1) of the prefill kernels, spread over the groups.
+// Each group rebases its state to its true row max: O_g beta_g, m_g = rmax
+// scale (natural log), l_g beta_g (both half rows); a group that saw no key
+// of a row has weight 0.  A lane's O is kC float4 chunks (chunk cc holds
+// d = 32 (cc / 4) + 8 (cc % 4) + 4 (l / 32) .. +3); group h owns chunks
+// [h kCPer, (h+1) kCPer).  Every group publishes (m_g, l_g) in merge_ml and
+// the chunks it does not own in lane-private 1 KiB slots (slot_base(k), in
+// the then free stage buffers); after one barrier every group merges and
+// stores its own chunks,
+//   O = sum_g w_g O_g / L,  L = sum_g w_g l_g,  w_g = exp(m_g - max m),
+// summing over g = 0 .. KS-1 in that order whatever the owner, so the result
+// does not depend on which group stores a chunk.  Opens with the barrier
+// after which every group is done with its stage regions.
+template <int D, int KS, int kRowWaves, class SlotBase>
+__device__ __forceinline__ void merge_kv_groups(const AttnParams& p, const RowState& st,
+                                                const f32x16 (&o)[D / 32], SlotBase slot_base,
+                                                float* merge_ml, int wave, int kgrp, int lane, int g,
+                                                size_t ri, bool row_ok) {
+    constexpr int kC = D / 32 * 4;                      // float4 chunks per lane
+    constexpr int kCPer = kC / KS;                      // chunks each group stores
+    static_assert(kC % KS == 0, "chunks per group");
+    // Slot of chunk cc of row wave w written by group gw (!= owner h).
+    auto slot = [&](int cc, int gw, int h) {
+        const int k = (wave * kC + cc) * (KS - 1) + (gw < h ? gw : gw - 1);
+        return reinterpret_cast<f32x4*>(slot_base(k)) + lane;
+    };
+    auto chunk = [&](int cc) {
+        const int td = cc / 4, i = cc % 4;
+        return f32x4{o[td][4 * i], o[td][4 * i + 1], o[td][4 * i + 2], o[td][4 * i + 3]};
+    };
+    const float l_pair = sum_xor32(st.l);
+    const bool none = st.rmax == -INFINITY;
+    const float m_g = none ? -INFINITY : st.rmax * p.scale;
+    const float beta = none ? 0.f : exp2_hw(st.m - st.rmax * p.scale_log2);
+    __syncthreads();  // every group is done with its stage regions
+    merge_ml[(kgrp * kRowWaves + wave) * 64 + lane] = m_g;
+    merge_ml[((KS + kgrp) * kRowWaves + wave) * 64 + lane] = l_pair * beta;
+#pragma unroll
+    for (int cc = 0; cc < kC; ++cc) {
+        const int h = cc / kCPer;
+        if (h != kgrp) *slot(cc, kgrp, h) = chunk(cc) * beta;
+    }
+    __syncthreads();
+    float m_all = -INFINITY;
+#pragma unroll
+    for (int gg = 0; gg < KS; ++gg) m_all = fmaxf(m_all, merge_ml[(gg * kRowWaves + wave) * 64 + lane]);
+    float wgt[KS];
+    float L = 0.f;
+#pragma unroll
+    for (int gg = 0; gg < KS; ++gg) {
+        const float mo = merge_ml[(gg * kRowWaves + wave) * 64 + lane];
+        wgt[gg] = mo == -INFINITY ? 0.f : exp2_hw((mo - m_all) * kLog2e);
+        L += wgt[gg] * merge_ml[((KS + gg) * kRowWaves + wave) * 64 + lane];
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    auto merge_store = [&](auto out) {
+        constexpr int kOut = decltype(out)::value;
+#pragma unroll
+        for (int cc = 0; cc < kC; ++cc) {
+            if (cc / kCPer != kgrp) continue;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int gg = 0; gg < KS; ++gg) {
+                const f32x4 v = gg == kgrp ? chunk(cc) * beta : *slot(cc, gg, kgrp);
+                acc = wgt[gg] * v + acc;
+            }
+            const int d = 32 * (cc / 4) + 8 * (cc % 4) + 4 * g;
+            if (row_ok && d < D) store_out4_as<kOut>(p, ri * D + d, acc * inv);
+        }
+    };
+    if (p.out_dtype == kOutF16)
+        merge_store(std::integral_constant<int, kOutF16>{});
+    else if (p.out_dtype == kOutBF16)
+        merge_store(std::integral_constant<int, kOutBF16>{});
+    else
+        merge_store(std::integral_constant<int, kOutF32>{});
+    if (kgrp == 0 && row_ok && g == 0) store_stats(p, ri, m_all, L);
+}
+
 // kMask: causal masking and/or per-sequence key counts (p.causal,
 // p.kv_lens); without it every row sees keys [0, kv_len).
 //
@@ -1171,82 +1250,17 @@ void kf_attn_prefill_kernel(AttnParams p) {
     }
 
     if constexpr (KS > 1) {
-        // ---- KV-group merge, spread over the groups.  Each group rebases its
-        // state to its true row max: O_g beta_g, m_g = rmax scale (natural
-        // log), l_g beta_g (both half rows); a group that saw no key of a row
-        // has weight 0.  A lane's O is kC float4 chunks (chunk cc holds
-        // d = 32 (cc / 4) + 8 (cc % 4) + 4 (l / 32) .. +3); group h owns
-        // chunks [h kCPer, (h+1) kCPer).  Every group publishes (m_g, l_g)
-        // and the chunks it does not own in lane-private 1 KiB slots of the
-        // (now free) stage buffers; after one barrier every group merges and
-        // stores its own chunks,
-        //   O = sum_g w_g O_g / L,  L = sum_g w_g l_g,  w_g = exp(m_g - max m),
-        // summing over g = 0 .. KS-1 in that order whatever the owner, so the
-        // result does not depend on which group stores a chunk.
-        constexpr int kC = kNTD * 4;                        // float4 chunks per lane
-        constexpr int kCPer = kC / KS;                      // chunks each group stores
+        static_assert(kRowWaves * kNTD * 4 * (KS - 1) <= Cfg::kBuffers * KS * S::kStageBytes / 1024,
+                      "merge slots");
+        // Merge slot k: 1 KiB at k % per-buffer in stage buffer k / per-buffer.
         constexpr int kSlotsPerBuf = KS * S::kStageBytes / 1024;
-        static_assert(kC % KS == 0, "chunks per group");
-        static_assert(kRowWaves * kC * (KS - 1) <= Cfg::kBuffers * kSlotsPerBuf, "merge slots");
-        __shared__ float merge_ml[2 * KS * kRowWaves * 64];
-        // Slot of chunk cc of row wave w written by group gw (!= owner h).
-        auto slot = [&](int cc, int gw, int h) {
-            const int k = (wave * kC + cc) * (KS - 1) + (gw < h ? gw : gw - 1);
+        auto slot_base = [&](int k) {
             char* bb = k / kSlotsPerBuf == 0 ? buf0 : (k / kSlotsPerBuf == 1 ? buf1 : buf2);
-            return reinterpret_cast<f32x4*>(bb + (k % kSlotsPerBuf) * 1024) + lane;
+            return bb + (k % kSlotsPerBuf) * 1024;
         };
-        auto chunk = [&](int cc) {
-            const int td = cc / 4, i = cc % 4;
-            return f32x4{o[td][4 * i], o[td][4 * i + 1], o[td][4 * i + 2], o[td][4 * i + 3]};
-        };
-        const float l_pair = sum_xor32(st.l);
-        const bool none = st.rmax == -INFINITY;
-        const float m_g = none ? -INFINITY : st.rmax * p.scale;
-        const float beta = none ? 0.f : exp2_hw(st.m - st.rmax * p.scale_log2);
-        __syncthreads();  // every group is done with its stage regions
-        merge_ml[(kgrp * kRowWaves + wave) * 64 + lane] = m_g;
-        merge_ml[((KS + kgrp) * kRowWaves + wave) * 64 + lane] = l_pair * beta;
-#pragma unroll
-        for (int cc = 0; cc < kC; ++cc) {
-            const int h = cc / kCPer;
-            if (h != kgrp) *slot(cc, kgrp, h) = chunk(cc) * beta;
-        }
-        __syncthreads();
-        float m_all = -INFINITY;
-#pragma unroll
-        for (int gg = 0; gg < KS; ++gg) m_all = fmaxf(m_all, merge_ml[(gg * kRowWaves + wave) * 64 + lane]);
-        float wgt[KS];
-        float L = 0.f;
-#pragma unroll
-        for (int gg = 0; gg < KS; ++gg) {
-            const float mo = merge_ml[(gg * kRowWaves + wave) * 64 + lane];
-            wgt[gg] = mo == -INFINITY ? 0.f : exp2_hw((mo - m_all) * kLog2e);
-            L += wgt[gg] * merge_ml[((KS + gg) * kRowWaves + wave) * 64 + lane];
-        }
-        const float inv = L > 0.f ? 1.0f / L : 0.f;
-        const size_t ri = (size_t)grp * R + row;
-        auto merge_store = [&](auto out) {
-            constexpr int kOut = decltype(out)::value;
-#pragma unroll
-            for (int cc = 0; cc < kC; ++cc) {
-                if (cc / kCPer != kgrp) continue;
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int gg = 0; gg < KS; ++gg) {
-                    const f32x4 v = gg == kgrp ? chunk(cc) * beta : *slot(cc, gg, kgrp);
-                    acc = wgt[gg] * v + acc;
-                }
-                const int d = 32 * (cc / 4) + 8 * (cc % 4) + 4 * g;
-                if (row < R && d < D) store_out4_as<kOut>(p, ri * D + d, acc * inv);
-            }
-        };
-        if (p.out_dtype == kOutF16)
-            merge_store(std::integral_constant<int, kOutF16>{});
-        else if (p.out_dtype == kOutBF16)
-            merge_store(std::integral_constant<int, kOutBF16>{});
-        else
-            merge_store(std::integral_constant<int, kOutF32>{});
-        if (kgrp == 0 && row < R && g == 0) store_stats(p, ri, m_all, L);
+        __shared__ float merge_ml[2 * KS * kRowWaves * 64];
+        merge_kv_groups<D, KS, kRowWaves>(p, st, o, slot_base, merge_ml, wave, kgrp, lane, g,
+                                          (size_t)grp * R + row, row < R);
         return;
     }
 
@@ -1304,9 +1318,12 @@ template <int D> struct WideCfg {
 // kf_attn_prefill_kernel.  Causal masking needs one row block per wave
 // (D = 256); with two (D = 64 / 128) the host launches the masked kernel
 // for key counts only, which give every row of a sequence the same limit.
+// KS > 1 (D = 256): KV groups as in kf_attn_prefill_kernel — the waves form
+// KS groups of NW / KS, each on the same rows and its own share of the keys,
+// merged through LDS at the end; for grids too small for 256-row tiles.
 // (The body sits in the kernel itself: moved into a shared device function,
 // the unmasked kernel compiled to a different, 0.5 % slower schedule.)
-template <int D, bool kMask>
+template <int D, bool kMask, int KS>
 __global__ __launch_bounds__(WideCfg<D>::kThreads, 2)
 void kf_attn_prefill_wide_kernel(AttnParams p) {
     static_assert(D == 64 || D == 128 || D == 256, "wide prefill: D = 64, 128 or 256");
@@ -1314,18 +1331,23 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     constexpr int NW = Cfg::kWaves;
     constexpr int BC = Cfg::BC;
     constexpr int SR = Cfg::kStageRows;
-    constexpr int kRows = Cfg::kRows;
     constexpr bool kQ1Lds = Cfg::kQ1Lds;
     constexpr bool kPipe = Cfg::kPipe;
     constexpr int kRB = Cfg::kRB;
     constexpr bool kXorOff = Cfg::kXorOff;
-    using S = DmaStage<D, SR, NW>;
+    static_assert(KS == 1 || (KS == 2 && kRB == 1 && !kPipe && SR == BC), "KV groups: D = 256, two groups");
+    constexpr int kRowWaves = NW / KS;                 // waves per KV group
+    constexpr int kRows = 32 * kRB * kRowWaves;        // query rows per workgroup
+    using S = DmaStage<D, SR, kRowWaves>;
     using SW = SwizzleRow<D>;
     constexpr int kNKK = D / 16;
     constexpr int kNTD = D / 32;
     constexpr int kHalfRows = kRows / 2;           // rows of one row block, all waves
-    __shared__ __attribute__((aligned(1024))) char buf0[S::kStageBytes];
-    __shared__ __attribute__((aligned(1024))) char buf1[S::kStageBytes];
+    // KS > 1: buf0 holds group g's two stage regions at 2 g and 2 g + 1
+    // (the offset between them fits the LDS reads' immediate) and, after
+    // the loop, the merge slots.
+    __shared__ __attribute__((aligned(1024))) char buf0[(KS == 1 ? 1 : 2 * KS) * S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char buf1[KS == 1 ? S::kStageBytes : 16];
     __shared__ __attribute__((aligned(1024))) char buf2[kPipe ? S::kStageBytes : 16];
     // The stage buffers come first (the backend orders LDS variables by
     // alignment), so their addresses fit the 16-bit immediate offset of the
@@ -1340,7 +1362,8 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     // same count on every SIMD.
     // Causal masking is compiled in for one row block per wave only.
     const bool causal = kMask && kRB == 1 && p.causal;
-    const int wave = (causal && wave_id >= 4) ? 11 - wave_id : wave_id;
+    const int wave = KS == 1 ? ((causal && wave_id >= 4) ? 11 - wave_id : wave_id) : wave_id % kRowWaves;
+    const int kgrp = KS == 1 ? 0 : wave_id / kRowWaves;  // KV group
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x, p.xcds);
     int rt = blk % p.row_tiles;
@@ -1382,36 +1405,48 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             }
         }
     }
-    const int ntiles = (blk_lim + BC - 1) / BC;
-    const int nstages = (blk_lim + SR - 1) / SR;
+    // KV group kgrp covers the keys [kv_base, kv_end) of the workgroup's
+    // range in tiles 0 .. ntiles - 1 (the same count for every group, so the
+    // barriers line up); row limits below are relative to kv_base.
+    const int ntiles_wg = (blk_lim + BC - 1) / BC;
+    const int ntiles = KS == 1 ? ntiles_wg : (ntiles_wg + KS - 1) / KS;
+    const int nstages = KS == 1 ? (blk_lim + SR - 1) / SR : (ntiles * BC + SR - 1) / SR;
+    const int kv_base = kgrp * ntiles * BC;
+    const int kv_end = min(kv_base + ntiles * BC, blk_lim);
+    if constexpr (KS > 1) wave_min = min(wave_min, kv_end) - kv_base;
     // Tiles with a key visible to some row of this wave; the later ones are
     // skipped (their scores would add exactly nothing), the wave still
     // taking part in the stage barriers and copies.
-    const int nt_w = kMask ? min(ntiles, (wave_max + BC - 1) / BC) : ntiles;
+    const int wmax = KS == 1 ? wave_max : min(wave_max, kv_end) - kv_base;
+    const int nt_w = kMask ? min(ntiles, (wmax + BC - 1) / BC) : ntiles;
+    char* const b0 = KS == 1 ? buf0 : buf0 + 2 * kgrp * S::kStageBytes;  // this group's stages
+    char* const b1 = KS == 1 ? buf1 : b0 + S::kStageBytes;
 
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
     const char* Kh = reinterpret_cast<const char*>(p.K + (size_t)grp * kv_len * D);
     const char* Vh = reinterpret_cast<const char*>(p.V + (size_t)grp * kv_len * D);
 
-    // LDS-DMA plan as in kf_attn_prefill_kernel: wave w issues the KiB
-    // instructions j = w + NW i of a stage (K region, then V region).
+    // LDS-DMA plan as in kf_attn_prefill_kernel: wave w of a group issues
+    // the KiB instructions j = w + kRowWaves i of the group's stage (K
+    // region, then V region).
     constexpr int kLaneBases = S::kRowsPerInstr >= 16 ? 1 : 16 / S::kRowsPerInstr;
-    constexpr int kLBPeriod = kLaneBases / gcd_int(NW, kLaneBases);
+    constexpr int kLBPeriod = kLaneBases / gcd_int(kRowWaves, kLaneBases);
     uint32_t lane_base[kLBPeriod];
 #pragma unroll
     for (int i = 0; i < kLBPeriod; ++i) {
-        const int ii = (wave + NW * i) % S::kInstrPerTensor;
+        const int ii = (wave + kRowWaves * i) % S::kInstrPerTensor;
         const int lr = lane / S::kChunks;
         const int r = ii * S::kRowsPerInstr + lr;
         lane_base[i] = (uint32_t)(lr * S::kRowBytes +
                                   (((lane % S::kChunks) ^ SW::h(r)) % S::kChunks) * 16);
     }
-    auto issue_stage = [&](char* dst, int kv0) {
+    auto issue_stage = [&](char* dst, int kv0_rel) {
+        const int kv0 = kv_base + kv0_rel;
         if (kv0 + SR <= kv_len) {
 #pragma unroll
             for (int i = 0; i < S::kPerWave; ++i) {
-                const int j = wave + NW * i;
-                if (S::kInstrTotal % NW == 0 || j < S::kInstrTotal) {
+                const int j = wave + kRowWaves * i;
+                if (S::kInstrTotal % kRowWaves == 0 || j < S::kInstrTotal) {
                     const bool is_v = j >= S::kInstrPerTensor;
                     const int ii = j % S::kInstrPerTensor;
                     const char* base = (is_v ? Vh : Kh) + (size_t)(kv0 + ii * S::kRowsPerInstr) * S::kRowBytes;
@@ -1428,8 +1463,8 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             const int lr = lane / S::kChunks;
 #pragma unroll
             for (int i = 0; i < S::kPerWave; ++i) {
-                const int j = wave + NW * i;
-                if (S::kInstrTotal % NW == 0 || j < S::kInstrTotal) {
+                const int j = wave + kRowWaves * i;
+                if (S::kInstrTotal % kRowWaves == 0 || j < S::kInstrTotal) {
                     const bool is_v = j >= S::kInstrPerTensor;
                     const int ii = j % S::kInstrPerTensor;
                     const int kv = min(kv0 + ii * S::kRowsPerInstr + lr, kv_len - 1);
@@ -1483,7 +1518,7 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
 #pragma unroll
         for (int b = 0; b < kRB; ++b) {
             const int row = b == 0 ? row0 : row1;
-            if (row < R) {
+            if (row < R && kgrp == 0) {
                 const size_t ri = (size_t)grp * R + row;
 #pragma unroll
                 for (int td = 0; td < kNTD; ++td)
@@ -1498,8 +1533,9 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     // This lane's query row sees keys [0, lim_lane) (padding rows: blk_lim).
     int lim_lane = kv_len;
     if constexpr (kMask) lim_lane = !causal ? kvb : row0 < R ? row_kv_limit(p, kvb, row0 % p.q_len) : blk_lim;
+    if constexpr (KS > 1) lim_lane = min(lim_lane, kv_end) - kv_base;
 
-    issue_stage(buf0, 0);
+    issue_stage(b0, 0);
     f16x8 q0[kNKK], q1[(kRB == 2 && !kQ1Lds) ? kNKK : 1];
     load_q_frags<D>(Qg, row0, R, lane, q0);
     if constexpr (kQ1Lds) {
@@ -1601,9 +1637,10 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             tail_mask(s0, s1, t);
             f16x8 p0[2], p1[2];
             block_update_max<kNTD>(st0, block_rowmax<1>(s0), c, inv_c, o0);
-            // A row that has seen no key yet (masked) keeps m = -inf and must
-            // get P = 0, not NaN.
-            block_exp(s0[0], c, (kMask && st0.m == -INFINITY) ? 0.f : -st0.m, p0[0], p0[1], st0.l);
+            // A row that has seen no key yet (masked, or a KV group's tiles
+            // past the keys) keeps m = -inf and must get P = 0, not NaN.
+            block_exp(s0[0], c, ((kMask || KS > 1) && st0.m == -INFINITY) ? 0.f : -st0.m, p0[0], p0[1],
+                      st0.l);
             if constexpr (kRB == 2) {
                 block_update_max<kNTD>(st1, block_rowmax<1>(s1), c, inv_c, o1);
                 block_exp(s1[0], c, -st1.m, p1[0], p1[1], st1.l);
@@ -1617,8 +1654,8 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             for (int u = 0; u < 2; ++u) {
                 const int j = js + u;
                 if (j >= nstages) break;
-                char* cur = u == 0 ? buf0 : buf1;
-                char* nxt = u == 0 ? buf1 : buf0;
+                char* cur = u == 0 ? b0 : b1;
+                char* nxt = u == 0 ? b1 : b0;
                 // Stage j (and, at j = 0, the block-1 query rows) landed for
                 // every wave; every wave is done with stage j-1 (in nxt).
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1679,6 +1716,16 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             if (t + 5 >= ntiles) break;
             tile(buf2 + H, buf0, buf1, t + 5, true);
         }
+    }
+
+    if constexpr (KS > 1) {
+        // Merge slot k: 1 KiB at k * 1024 of buf0 (every group's stages).
+        static_assert(kRowWaves * kNTD * 4 * (KS - 1) <= 2 * KS * S::kStageBytes / 1024, "merge slots");
+        auto slot_base = [&](int k) { return buf0 + k * 1024; };
+        __shared__ float merge_ml[2 * KS * kRowWaves * 64];
+        merge_kv_groups<D, KS, kRowWaves>(p, st0, o0, slot_base, merge_ml, wave, kgrp, lane, g,
+                                          (size_t)grp * R + row0, row0 < R);
+        return;
     }
 
     // ---- Epilogue: both row blocks (unmasked, every row saw key 0, so l > 0). ----

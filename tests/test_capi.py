@@ -170,7 +170,7 @@ def test_plans_for_baseline_configs():
     assert p.path == "prefill" and p.rows_per_group == 4 * 4096
     assert p.block_threads == 512                    # 8 waves x 64 query rows
     assert p.grid_blocks == 8 * (4 * 4096 // 512) == 256
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false, 1>"
     # masked: the 256-row kernel (8 waves x 32 rows), 512 workgroups
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == "kf_attn_prefill_kernel<128, true, 8, 1>"
     p = kf.plan(1, 2048, 2048, 32, 8, 128)           # S = 2048: 128 wide workgroups would idle CUs
@@ -251,7 +251,7 @@ def test_decode_split_counts(B, H_kv, kv, D, splits, per_block):
 @pytest.mark.parametrize("S,H_kv,D,waves,groups", [
     (4096, 8, 128, 8, 1), (2048, 8, 128, 8, 1), (1024, 8, 128, 8, 2), (512, 8, 128, 8, 4),
     (256, 8, 128, 4, 2), (100, 8, 128, 2, 1), (2048, 1, 64, 8, 1), (512, 1, 64, 8, 4), (1024, 1, 64, 8, 2),
-    (130, 2, 256, 4, 1), (4096, 8, 256, 4, 1),
+    (130, 2, 256, 4, 1), (4096, 8, 256, 4, 1), (512, 8, 256, 4, 1), (2048, 4, 256, 4, 1),
 ])
 def test_prefill_waves_per_workgroup(S, H_kv, D, waves, groups):
     """Waves and KV groups per workgroup (32 query rows per wave of a KV
@@ -267,14 +267,21 @@ def test_prefill_waves_per_workgroup(S, H_kv, D, waves, groups):
     # Masked calls run this kernel at D = 64 / 128; unmasked ones, and masked
     # ones at D = 256, may run a wide kernel instead (test_wide_prefill_selection).
     masked_name = kf.kernel_names(1, S, S, 32, H_kv, D, causal=True)
-    if wide and D == 256:
-        assert masked_name == "kf_attn_prefill_wide_kernel<256, true>"
-    else:
-        assert masked_name == f"kf_attn_prefill_kernel<{D}, true, {waves}, {groups}>"
     rows = 32 * waves // groups
     R = 32 // H_kv * S
+    # D = 256: 256-row tiles when they take fewer rounds (at 0.7 of the time
+    # per row), else, from 256 keys on, two KV groups on the 128-row tiles.
+    ks = 0
+    if D == 256:
+        n128, n256 = H_kv * -(-R // 128), H_kv * -(-R // 256)
+        ks = 1 if -(-n256 // 256) * 256 * 0.7 < -(-n128 // 256) * 128 else 2 if S >= 256 else 0
+        assert wide == (ks > 0)
+    if wide and D == 256:
+        assert masked_name == f"kf_attn_prefill_wide_kernel<256, true, {ks}>"
+    else:
+        assert masked_name == f"kf_attn_prefill_kernel<{D}, true, {waves}, {groups}>"
     if wide:
-        assert p.grid_blocks == H_kv * -(-R // (256 if D == 256 else 512))
+        assert p.grid_blocks == H_kv * -(-R // (512 if D != 256 else 256 if ks == 1 else 128))
     else:
         assert kf.kernel_names(1, S, S, 32, H_kv, D) == \
             f"kf_attn_prefill_kernel<{D}, false, {waves}, {groups}>"
@@ -381,19 +388,21 @@ def test_plan_for_cus_rejects_bad_counts(lib):
 def test_kernel_names_follow_the_plan(lib):
     """kf_attn_kernel_names names the kernels in launch order, as the
     profiler lists them."""
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, masked=True) == "kf_attn_prefill_wide_kernel<128, true>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, masked=True) == "kf_attn_prefill_wide_kernel<128, true, 1>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 2048, 2048, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 1>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == \
         "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 512, 512, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 4>"
     assert kf.kernel_names(1, 256, 256, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 4, 2>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_wide_kernel<256, false>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, causal=True) == "kf_attn_prefill_wide_kernel<256, true>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, masked=True) == "kf_attn_prefill_wide_kernel<256, true>"
-    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256) == "kf_attn_prefill_kernel<256, false, 4, 1>"
-    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256, causal=True) == "kf_attn_prefill_kernel<256, true, 4, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_wide_kernel<256, false, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, causal=True) == "kf_attn_prefill_wide_kernel<256, true, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, masked=True) == "kf_attn_prefill_wide_kernel<256, true, 1>"
+    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256) == "kf_attn_prefill_wide_kernel<256, false, 2>"
+    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256, causal=True) == "kf_attn_prefill_wide_kernel<256, true, 2>"
+    assert kf.kernel_names(1, 2048, 255, 16, 4, 256) == "kf_attn_prefill_kernel<256, false, 4, 1>"
+    assert kf.kernel_names(1, 2048, 255, 16, 4, 256, causal=True) == "kf_attn_prefill_kernel<256, true, 4, 1>"
     assert kf.kernel_names(1, 1, 4096, 32, 8, 128) == \
         "kf_attn_decode_short_kernel<128, 1> + kf_attn_split_merge_kernel<128, 8, 4>"
     assert kf.kernel_names(32, 1, 8192, 32, 8, 128) == "kf_attn_decode_kernel<128, false>"

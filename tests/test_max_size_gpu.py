@@ -7,7 +7,9 @@ the last V row exactly, while every other V row holds -1; Mi must be that
 score and Li exactly 1.  A wrapped or truncated offset would read another
 row and show up as -1 / a wrong Mi.  Run through the decode kernels, the
 small-grid prefill and (65792 / 32896 query rows) the wide prefill kernel
-at D = 128 and 256, unmasked and masked (key count = kv_len)."""
+at D = 128 and 256, unmasked and masked (key count = kv_len), and (64 rows,
+D = 256) the wide kernel with two KV groups, whose second group starts at
+key kv_len / 2."""
 import math
 
 import pytest
@@ -18,19 +20,22 @@ import kernelfoundry_amd as kf
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("q_len,H_q,D", [(1, 8, 128), (64, 1, 128), (1, 8, 256),
+@pytest.mark.parametrize("q_len,H_q,D", [(1, 8, 128), (64, 1, 128), (1, 8, 256), (64, 1, 256),
                                          (2056, 32, 128), (1028, 32, 256)])
 def test_last_key_at_the_offset_limit(q_len, H_q, D):
     kv = (2 ** 31 - 1) // D // 64 * 64 - 64
     names = kf.kernel_names(1, q_len, kv, H_q, 1, D)
     print("case", dict(q_len=q_len, H_q=H_q, D=D, kv=kv, path=kf.plan(1, q_len, kv, H_q, 1, D).path,
                        kernels=names), flush=True)
-    wide = q_len > 1000  # 65792 / 32896 rows: the wide prefill kernel
+    # 65792 / 32896 rows: the wide prefill kernel; 64 rows at D = 256: its
+    # KV-group form
+    wide = q_len > 1000 or (q_len == 64 and D == 256)
     if wide:
-        assert names.startswith("kf_attn_prefill_wide_kernel"), names
+        ks = 1 if q_len > 1000 else 2
+        assert names == f"kf_attn_prefill_wide_kernel<{D}, false, {ks}>", names
         # ... and its masked instantiation, with the key count set to kv_len
         masked = kf.kernel_names(1, q_len, kv, H_q, 1, D, masked=True)
-        assert masked == f"kf_attn_prefill_wide_kernel<{D}, true>", masked
+        assert masked == f"kf_attn_prefill_wide_kernel<{D}, true, {ks}>", masked
     dev = torch.device("cuda")
     K = torch.zeros((1, 1, kv, D), dtype=torch.float16, device=dev)
     V = torch.full((1, 1, kv, D), -1.0, dtype=torch.float16, device=dev)

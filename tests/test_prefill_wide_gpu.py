@@ -1,6 +1,7 @@
-"""GPU parity of the wide prefill kernel (kf_attn_prefill_wide_kernel<D, kMask>: 8
+"""GPU parity of the wide prefill kernel (kf_attn_prefill_wide_kernel<D, kMask, KS>: 8
 waves x 64 query rows, 512 rows per workgroup, at D = 64 and 128; 8 waves x
-32 rows at D = 256).
+32 rows at D = 256; KS = 2, D = 256 only: two KV groups of 4 waves on 128
+rows, each on its half of every row's keys).
 
 The planner runs it for unmasked calls when its grid finishes in less time
 than the narrower kernel's (rounds of one workgroup per CU); every shape
@@ -20,7 +21,7 @@ equal, bit for bit, that kernel's on the same inputs (PAIRS, below), and
 the masked wide kernel with every sequence's key count equal to kv_len must
 give the unmasked one's bits.
 
-Masked calls run kf_attn_prefill_wide_kernel<D, true> when the planner
+Masked calls run kf_attn_prefill_wide_kernel<D, true, 1> when the planner
 chooses the wide grid: at D = 256 causal and/or per-sequence key counts, at
 D = 64 / 128 key counts only (causal calls keep the 256-row kernel).
 MASKED_CASES cover causal with q_len = kv_len, kv_len > q_len and q_len >
@@ -29,6 +30,16 @@ key, both together, and GQA ratio 16, against the oracle with rows without
 keys exactly O = 0, Mi = -inf, Li = 0.  PAIRS check the wide kernels
 against the 32-row kernel bit for bit through the planner's own choice
 (B = 1 plans the 32-row kernel, B = 2 the wide one, at the same shape).
+
+GROUP_CASES: the KV-group kernel (D = 256 grids that the 256-row tiles would
+leave with idle CUs, from 256 keys on), unmasked and masked, against the
+oracle: an odd tile count (the second group's last tile wholly past the
+keys), a group with no key at all (key count 31, causal rows near the top),
+empty sequences and rows, padding rows, MHA / GQA / MQA, and (max-size
+test) keys at the 32-bit offset limit.  Its groups merge in another order
+than any one-group kernel, so it is held to the oracle bar, not bit
+equality; the masked kernel with key counts = kv_len still gives the
+unmasked one's bits.
 """
 import numpy as np
 import pytest
@@ -79,7 +90,7 @@ def test_wide_prefill_matches_oracle(case):
     B, H_q, H_kv, q_len, kv_len, D = case
     names = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D)
     print("case", case, names, flush=True)
-    assert names == f"kf_attn_prefill_wide_kernel<{D}, false>", names
+    assert names == f"kf_attn_prefill_wide_kernel<{D}, false, 1>", names
     (q16, k16, v16), (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 11 + kv_len)
     O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True)
     torch.cuda.synchronize()
@@ -100,7 +111,7 @@ def test_wide_masked_without_masking_equals_unmasked_bitwise(case):
     B, H_q, H_kv, q_len, kv_len, D = case
     masked = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, masked=True)
     print("case", case, masked, flush=True)
-    assert masked == f"kf_attn_prefill_wide_kernel<{D}, true>", masked
+    assert masked == f"kf_attn_prefill_wide_kernel<{D}, true, 1>", masked
     _, (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 5)
     full = torch.full((B,), kv_len, dtype=torch.int32, device="cuda")
     Ow, Mw, Lw = kf.attn_fwd(Q, K, V, return_stats=True)
@@ -134,43 +145,93 @@ def test_wide_masked_prefill_matches_oracle(case):
     B, H_q, H_kv, q_len, kv_len, causal, kv_lens, D = case
     name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, causal=causal, masked=kv_lens is not None)
     print("case", case, name, flush=True)
-    assert name == f"kf_attn_prefill_wide_kernel<{D}, true>", name
+    assert name == f"kf_attn_prefill_wide_kernel<{D}, true, 1>", name
     run_and_check(B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens, 300 + q_len)
 
 
-# At S = 2048 the planner runs the 256-row kernel (the 128-row one at
-# D = 256) for B = 1 and the wide kernel for B = 2: batch 0 of the B = 2 call
-# holds the B = 1 call's inputs, so its O, Mi and Li must be the same bits.
+# At q_len = 2048 the planner runs the 256-row kernel (the 128-row one at
+# D = 256, below 256 keys) for B = 1 and the wide kernel for B = 2: batch 0
+# of the B = 2 call holds the B = 1 call's inputs, so its O, Mi and Li must
+# be the same bits.
 PAIRS = [
-    # D, H_q, H_kv, causal, batch-0 key count (None: unmasked)
-    (128, 32, 8, False, None),
-    (128, 32, 8, False, 1500),
-    (64, 32, 8, False, None),
-    (64, 32, 8, False, 777),
-    (256, 16, 4, False, None),
-    (256, 16, 4, False, 1111),
-    (256, 16, 4, True, None),
+    # D, H_q, H_kv, kv_len, causal, batch-0 key count (None: unmasked)
+    (128, 32, 8, 2048, False, None),
+    (128, 32, 8, 2048, False, 1500),
+    (64, 32, 8, 2048, False, None),
+    (64, 32, 8, 2048, False, 777),
+    (256, 16, 4, 200, False, None),
+    (256, 16, 4, 255, False, 150),
+    (256, 16, 4, 255, True, None),     # rows 1793.. see keys
 ]
 
 
-@pytest.mark.parametrize("case", PAIRS, ids=lambda c: "D{}_Hq{}_Hkv{}_c{}_{}".format(
-    c[0], c[1], c[2], int(c[3]), "full" if c[4] is None else f"k{c[4]}"))
+@pytest.mark.parametrize("case", PAIRS, ids=lambda c: "D{}_Hq{}_Hkv{}_kv{}_c{}_{}".format(
+    c[0], c[1], c[2], c[3], int(c[4]), "full" if c[5] is None else f"k{c[5]}"))
 def test_wide_and_narrow_kernels_agree_bitwise(case):
     import kernelfoundry_amd as kf
     torch = _torch()
-    D, H_q, H_kv, causal, k0 = case
+    D, H_q, H_kv, kv, causal, k0 = case
     S = 2048
     masked = k0 is not None
-    n1 = kf.kernel_names(1, S, S, H_q, H_kv, D, causal=causal, masked=masked)
-    n2 = kf.kernel_names(2, S, S, H_q, H_kv, D, causal=causal, masked=masked)
+    n1 = kf.kernel_names(1, S, kv, H_q, H_kv, D, causal=causal, masked=masked)
+    n2 = kf.kernel_names(2, S, kv, H_q, H_kv, D, causal=causal, masked=masked)
     print("case", case, n1, "|", n2, flush=True)
     assert n1.startswith("kf_attn_prefill_kernel<") and n2.startswith("kf_attn_prefill_wide_kernel<"), (n1, n2)
-    _, (Q, K, V) = _inputs(2, H_q, H_kv, S, S, D, 77)
+    assert n2.endswith(", 1>"), n2  # one KV group: the 32-row kernel's operation order
+    _, (Q, K, V) = _inputs(2, H_q, H_kv, S, kv, D, 77)
     l1 = torch.tensor([k0], dtype=torch.int32, device="cuda") if masked else None
-    l2 = torch.tensor([k0, S - 5], dtype=torch.int32, device="cuda") if masked else None
+    l2 = torch.tensor([k0, kv - 5], dtype=torch.int32, device="cuda") if masked else None
     O1, M1, L1 = kf.attn_fwd(Q[:1].contiguous(), K[:1].contiguous(), V[:1].contiguous(), return_stats=True,
                              causal=causal, kv_lens=l1)
     O2, M2, L2 = kf.attn_fwd(Q, K, V, return_stats=True, causal=causal, kv_lens=l2)
     torch.cuda.synchronize()
     assert torch.equal(O1[0], O2[0]), f"O differs: max {(O1[0] - O2[0]).abs().max().item():.3g}"
     assert torch.equal(M1[0], M2[0]) and torch.equal(L1[0], L2[0]), "Mi / Li differ"
+
+
+GROUP_CASES = [
+    # B, H_q, H_kv, q_len, kv_len, causal, kv_lens           what it hits
+    (1, 16, 4, 512, 512, False, None),                   # 16 tiles: 8 per group
+    (1, 16, 4, 300, 333, False, None),                   # 11 tiles: group 1's last past the keys; padding rows
+    (2, 8, 8, 256, 256, False, None),                    # MHA, 256 keys (the smallest KV-group case)
+    (1, 32, 1, 64, 1000, False, None),                   # MQA, 2048 rows, ragged keys
+    (2, 16, 4, 257, 257, False, None),                   # 9 tiles, group 1 from key 160
+    (1, 16, 4, 600, 600, True, None),                    # causal, ragged row tiles
+    (1, 16, 4, 600, 777, True, None),                    # causal, kv_len > q_len
+    (1, 16, 4, 700, 500, True, None),                    # causal, 200 rows without keys
+    (4, 16, 4, 300, 777, False, [777, 0, 31, 500]),      # key counts: empty; 31 keys (group 1 has none)
+    (4, 16, 4, 300, 700, True, [700, 129, 0, 640]),      # causal + key counts
+    (1, 32, 2, 300, 300, True, None),                    # GQA ratio 16, causal
+]
+
+
+def _gids(c):
+    return "B{}_Hq{}_Hkv{}_q{}_kv{}_c{}_{}".format(*c[:5], int(c[5]), "lens" if c[6] is not None else "full")
+
+
+@pytest.mark.parametrize("case", GROUP_CASES, ids=_gids)
+def test_kv_group_wide_prefill_matches_oracle(case):
+    import kernelfoundry_amd as kf
+    B, H_q, H_kv, q_len, kv_len, causal, kv_lens = case
+    mask = causal or kv_lens is not None
+    name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, 256, causal=causal, masked=kv_lens is not None)
+    print("case", case, name, flush=True)
+    assert name == f"kf_attn_prefill_wide_kernel<256, {'true' if mask else 'false'}, 2>", name
+    run_and_check(B, H_q, H_kv, q_len, kv_len, 256, causal, kv_lens, 900 + kv_len)
+
+
+@pytest.mark.parametrize("case", [c for c in GROUP_CASES if not c[5] and c[6] is None], ids=_gids)
+def test_kv_group_masked_without_masking_equals_unmasked_bitwise(case):
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    B, H_q, H_kv, q_len, kv_len = case[:5]
+    masked = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, 256, masked=True)
+    print("case", case, masked, flush=True)
+    assert masked == "kf_attn_prefill_wide_kernel<256, true, 2>", masked
+    _, (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, 256, 6)
+    full = torch.full((B,), kv_len, dtype=torch.int32, device="cuda")
+    Ow, Mw, Lw = kf.attn_fwd(Q, K, V, return_stats=True)
+    On, Mn, Ln = kf.attn_fwd(Q, K, V, return_stats=True, kv_lens=full)
+    torch.cuda.synchronize()
+    assert torch.equal(Ow, On), f"O differs: max {(Ow - On).abs().max().item():.3g}"
+    assert torch.equal(Mw, Mn) and torch.equal(Lw, Ln), "Mi / Li differ"
