@@ -37,8 +37,10 @@ half of the metric):
   * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep),
                      the MQA D=64 configs[3] and the configs[2] shape at
                      D=256 (the reference's largest head dimension), plain
-                     and causal (visible-pair FLOPs), and configs[2] with a
-                     per-sequence key count of 4000 (FLOPs over those keys).
+                     and causal (visible-pair FLOPs), S = 512 / 1024 at
+                     D=256 (small grids: two KV groups per workgroup), and
+                     configs[2] with a per-sequence key count of 4000 (FLOPs
+                     over those keys).  Each line names its kernel.
 
 FLOPs = 4*B*H_q*q_len*kv_len*D and bytes = fp16 Q + unique fp16 K,V + fp32 O
 (tests/bench_flash_attn.cu:125-131).  ``roofline.achieved`` divides those by
@@ -550,8 +552,7 @@ def main():
             out["causal"] = True
         if key_count is not None:
             out["key_count"] = key_count
-        if causal or key_count is not None:
-            out["kernels"] = kf.kernel_names(1, S, S, 32, H_kv, D, causal=causal, masked=key_count is not None)
+        out["kernels"] = kf.kernel_names(1, S, S, 32, H_kv, D, causal=causal, masked=key_count is not None)
         if check:
             out["parity"] = parity_spot_check(torch, r, check)
         return out
@@ -667,6 +668,7 @@ def main():
     sweep.append(run_prefill(2048, H_kv=1, D=64))
     sweep.append(run_prefill(4096, H_kv=8, D=256))
     sweep.append(run_prefill(4096, H_kv=8, D=256, causal=True))
+    sweep.extend(run_prefill(S, H_kv=8, D=256) for S in (512, 1024))
     # configs[2] with a per-sequence key count (kf_attn_fwd_ex kv_lens): the
     # sequence uses its first 4000 of the 4096 allocated key rows.
     sweep.append(run_prefill(4096, key_count=4000))
