@@ -9,7 +9,8 @@ the bits are the references).  LSE must equal Mi + ln(Li) of the fp32 call
 Mi + ln(Li) to 1e-3; rows without keys give LSE = -inf.
 
 Every kernel path that writes O is covered: prefill (unmasked and masked, the
-256-row and the wide kernel, masked by key counts and, at D = 256, causal),
+256-row and the wide kernel, masked by key counts and, at D = 256, causal;
+the KV-group merges of both kernels),
 decode without split (O written by the decode kernel), decode with split
 (O written by the merge kernel), and paged decode.
 """
@@ -44,6 +45,10 @@ CASES = [
     (1, 4, 4, 64, 64, 256, False, None),                  # prefill D=256
     (4, 32, 8, 600, 777, 128, False, [777, 0, 31, 500]),  # wide prefill with key counts
     (4, 16, 4, 700, 500, 256, True, None),                # wide prefill D=256, causal, rows without keys
+    (1, 16, 4, 300, 333, 256, False, None),               # wide prefill D=256, two KV groups (merge writes O)
+    (1, 16, 4, 700, 500, 256, True, None),                # the same, causal, rows without keys
+    (2, 16, 4, 300, 600, 256, False, [600, 31]),          # the same, key counts (one group without keys)
+    (1, 8, 2, 128, 600, 128, False, None),                # prefill, four KV groups of 8 waves
     (2, 8, 8, 1, 100, 16, False, None),                   # decode, one split
     (2, 32, 8, 1, 3000, 128, True, [3000, 7]),            # decode + merge kernel
 ]
