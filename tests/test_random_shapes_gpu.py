@@ -6,8 +6,9 @@ kernel (32- and 64-key splits) and the streaming decode kernel, each with and
 without the split merge, and the prefill kernel in every workgroup layout
 (8 waves x 256 rows, two KV groups of 8 or 4 waves, four KV groups of 8
 waves, 4 and 2 waves; D = 256 with 4 waves) and the wide prefill kernel (8
-waves x 64 rows, unmasked), with causal masking, per-sequence key counts (empty sequences
-included), ragged lengths and every head dimension.  Each case is
+waves x 64 rows at D = 64 / 128, 8 x 32 at D = 256, and at D = 256 its two
+KV groups of 4 waves), with causal masking, per-sequence key counts (empty
+sequences included), ragged lengths and every head dimension.  Each case is
 compared with oracle/attn_oracle.py's fp64 ``sdpa`` on the same fp16 inputs at
 the north-star bar (max |got - ref| <= 2e-3, ||got - ref|| / ||ref|| <= 1e-2;
 Mi to 1e-4, Li to 1e-3 relative; rows without keys exactly O = 0, Mi = -inf,
@@ -65,6 +66,10 @@ def _cases(n=40, seed=2026):
     # than the 256-row kernel's): D = 128 and 64, ragged key counts.
     out.append((32, 32, 8, 90, 150, 128, False, None, 21))
     out.append((16, 16, 4, 300, 333, 64, False, None, 22))
+    # D = 256: the wide kernel (256-row workgroups, causal) and its two-KV-group
+    # form unmasked (random D = 256 shapes reach it masked).
+    out.append((8, 32, 8, 150, 200, 256, True, None, 23))
+    out.append((1, 8, 2, 200, 700, 256, False, None, 24))
     return out
 
 
@@ -75,14 +80,14 @@ def _layout(kf, B, H_q, H_kv, q_len, kv_len, D, causal=False, masked=False):
     """(path, kernel) for decode, kernel "short32" / "short64" (one wave per
     split of that many keys) or "stream"; ("prefill", waves, kv_groups) for
     prefill, read from the kernel name (kf_attn_prefill_kernel<D, mask,
-    waves, kv_groups>), or ("prefill", "wide") for kf_attn_prefill_wide_kernel
+    waves, kv_groups>), or ("prefill", "wide", kv_groups) for kf_attn_prefill_wide_kernel
     with either mask flag."""
     p = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
     if p.path != "prefill":
         return (p.path, f"short{p.kv_per_split}" if p.splits_per_block == 4 else "stream")
     name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, causal=causal, masked=masked)
     if name.startswith("kf_attn_prefill_wide"):  # the wide kernel, masked or not
-        return ("prefill", "wide")
+        return ("prefill", "wide", int(name.rstrip(">").split(",")[-1]))
     waves, groups = (int(x) for x in name.rstrip(">").split(",")[-2:])
     return ("prefill", waves, groups)
 
@@ -94,7 +99,7 @@ def test_sweep_covers_every_dispatch():
     want = {("decode", "short32"), ("decode_split", "short32"), ("decode_split", "short64"),
             ("decode", "stream"), ("decode_split", "stream"),
             ("prefill", 8, 1), ("prefill", 8, 2), ("prefill", 8, 4), ("prefill", 4, 2), ("prefill", 4, 1),
-            ("prefill", 2, 1), ("prefill", "wide")}
+            ("prefill", 2, 1), ("prefill", "wide", 1), ("prefill", "wide", 2)}
     assert want <= seen, sorted(seen)
     # The split merge at its widest: 256 partials per row (4 columns per wave).
     assert any(kf.plan(c[0], c[3], c[4], c[1], c[2], c[5]).num_splits == 256 for c in CASES)
