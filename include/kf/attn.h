@@ -67,7 +67,9 @@ enum kf_status {
 enum kf_path {
     KF_PATH_PREFILL = 0,   /* MFMA prefill kernel, one pass over KV             */
     KF_PATH_DECODE = 1,    /* split-KV decode kernel, writes final O directly   */
-    KF_PATH_DECODE_SPLIT = 2 /* split-KV decode kernel + split-merge kernel      */
+    KF_PATH_DECODE_SPLIT = 2, /* split-KV decode kernel + split-merge kernel     */
+    KF_PATH_PREFILL_SPLIT = 3 /* MFMA prefill kernel over KV partitions (few query
+                                 rows, many keys) + split-merge kernel          */
 };
 
 typedef struct kf_attn_plan_t {

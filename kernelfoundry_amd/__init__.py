@@ -61,7 +61,7 @@ KF_ATTN_OUT_F16 = 2
 KF_ATTN_OUT_BF16 = 4
 KF_ATTN_LSE = 8
 
-PATH_NAMES = {0: "prefill", 1: "decode", 2: "decode_split"}
+PATH_NAMES = {0: "prefill", 1: "decode", 2: "decode_split", 3: "prefill_split"}
 
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1

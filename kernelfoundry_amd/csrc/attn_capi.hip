@@ -56,6 +56,14 @@ long long decode_stream_splits(long long n_groups, long long max_splits, int D, 
 constexpr long long kShortMaxWavesPerCU = 8;
 constexpr long long kShortMinWavesPerCU = 4;
 constexpr int kMinGroupKeys = 128;      // keys before a prefill row's keys are split between KV groups
+// Keys each KV group of a prefill workgroup keeps in a KV partition (split
+// prefill, below).
+constexpr int kMinSplitGroupKeys = 64;
+// Serial 32-key tiles per KV group a split prefill must save (measured at
+// 32 / 8 heads, D = 64 / 128: 4 saved tiles lose 3-22 %, 6 win 18-34 %).
+constexpr long long kMinSplitSavedTiles = 6;
+// kf_attn_fwd_noalloc's static scratch (split-KV partials), per device.
+constexpr size_t kStaticScratchBytes = size_t(16) << 20;
 // Time per query row of the wide prefill kernel relative to the 256-row
 // kernel (measured at S = 4096, 32 / 8 heads: 254 vs 267-271 us).
 constexpr double kWideRowCost = 0.94;
@@ -133,8 +141,18 @@ struct Plan {
 
 // paged: K/V come from a page pool (kf_attn_decode_paged), which only the
 // streaming decode kernel reads.  cus: compute units of the target device.
+// Workspace bytes of split partials (O, M, L) for `parts` (partition, row)
+// pairs.
+size_t split_ws_bytes(size_t parts, int D) {
+    return align_up(parts * D * sizeof(float), kWsAlign) + 2 * align_up(parts * sizeof(float), kWsAlign);
+}
+
+bool prefill_path(int path) { return path == KF_PATH_PREFILL || path == KF_PATH_PREFILL_SPLIT; }
+
+// ws_cap: most workspace the plan may ask for (split prefill only; the
+// split decode always fits kf_attn_fwd_noalloc's scratch).
 int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const DeviceShape& dev,
-              Plan* pl, bool paged = false) {
+              Plan* pl, bool paged = false, size_t ws_cap = SIZE_MAX) {
     const int cus = dev.cus;
     if (B <= 0 || q_len <= 0 || kv_len <= 0 || H_q <= 0 || H_kv <= 0 || cus <= 0) return KF_ERR_SIZE;
     if (!supported_head_dim(D)) return KF_ERR_HEAD_DIM;
@@ -255,8 +273,44 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
                 p.wide_kv_groups = 2;
             }
         }
+        // Few query rows per KV head against many keys (chunked prefill,
+        // speculative verification): a grid that leaves half the CUs or more
+        // without a workgroup also splits the keys across workgroups into KV
+        // partitions -- kf_attn_prefill_kernel writes split partials that
+        // the split-merge kernel combines, as on the split decode path -- as
+        // many as fit one round of workgroups while every KV group keeps
+        // kMinSplitGroupKeys keys of each partition (and the partials fit
+        // ws_cap), and only where that shortens each KV group's serial chain
+        // by kMinSplitSavedTiles 32-key tiles or more: the merge launch and
+        // the partials' round trip cost about that much.  D = 256 grids run
+        // the wide kernel's KV groups instead.
+        if (p.wide_row_tiles == 0 && D <= 128 && 2LL * p.grid <= cus) {
+            long long ns = cus / p.grid;
+            const long long by_keys = kv_len / ((long long)ks * kMinSplitGroupKeys);
+            if (ns > by_keys) ns = by_keys;
+            if (ns > kf::kMergeMaxSplits) ns = kf::kMergeMaxSplits;
+            while (ns > 1 && split_ws_bytes((size_t)ns * (size_t)rows_total, D) > ws_cap) --ns;
+            if (ns > 1) {
+                // Partition length: whole tiles for every KV group.
+                const long long unit = 32LL * ks;
+                long long per = (kv_len + ns - 1) / ns;
+                per = (per + unit - 1) / unit * unit;
+                ns = (kv_len + per - 1) / per;
+                const long long tiles = ((long long)kv_len + unit - 1) / unit;  // per KV group, unsplit
+                const long long saved = tiles - per / unit;
+                const int cw = kf::merge_cols(D, (int)ns);
+                if (ns > 1 && saved >= kMinSplitSavedTiles && (long long)p.grid * ns <= INT_MAX && rows_total * ((D / 4) / cw) <= INT_MAX) {
+                    p.n_splits = (int)ns;
+                    p.kv_per_split = (int)per;
+                    p.grid = (int)((long long)p.grid * ns);
+                    p.merge_cw = cw;
+                    p.merge_per = kf::merge_per_lane(cw, p.n_splits);
+                    p.path = KF_PATH_PREFILL_SPLIT;
+                }
+            }
+        }
     }
-    if (p.path == KF_PATH_DECODE_SPLIT) {
+    if (p.path == KF_PATH_DECODE_SPLIT || p.path == KF_PATH_PREFILL_SPLIT) {
         const size_t parts = (size_t)p.n_splits * (size_t)rows_total;
         p.ws_o_off = 0;
         p.ws_m_off = align_up(parts * D * sizeof(float), kWsAlign);
@@ -282,82 +336,72 @@ void launch_prefill(const Plan& pl, const kf::AttnParams& prm, bool mask, hipStr
         kf::kf_attn_prefill_kernel<D, false, NW, KS><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
 }
 
+// The prefill kernel of the plan (either prefill path).
 template <int D>
-hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t stream) {
-    if (pl.path == KF_PATH_PREFILL) {
-        const bool mask = prm.causal || prm.kv_lens;
-        if constexpr (D >= 256) {
-            if (pl.wide_row_tiles > 0) {
-                kf::AttnParams pw = prm;
-                pw.row_tiles = pl.wide_row_tiles;
-                const dim3 grid(pl.wide_grid), block(kf::WideCfg<D>::kThreads);
-                if (pl.wide_kv_groups == 2) {
-                    if (mask)
-                        kf::kf_attn_prefill_wide_kernel<D, true, 2><<<grid, block, 0, stream>>>(pw);
-                    else
-                        kf::kf_attn_prefill_wide_kernel<D, false, 2><<<grid, block, 0, stream>>>(pw);
-                } else if (mask) {
-                    kf::kf_attn_prefill_wide_kernel<D, true, 1><<<grid, block, 0, stream>>>(pw);
-                } else {
-                    kf::kf_attn_prefill_wide_kernel<D, false, 1><<<grid, block, 0, stream>>>(pw);
-                }
+hipError_t launch_prefill_kernel(const Plan& pl, const kf::AttnParams& prm, hipStream_t stream) {
+    const bool mask = prm.causal || prm.kv_lens;
+    if constexpr (D >= 256) {
+        if (pl.wide_row_tiles > 0) {
+            kf::AttnParams pw = prm;
+            pw.row_tiles = pl.wide_row_tiles;
+            const dim3 grid(pl.wide_grid), block(kf::WideCfg<D>::kThreads);
+            if (pl.wide_kv_groups == 2) {
+                if (mask)
+                    kf::kf_attn_prefill_wide_kernel<D, true, 2><<<grid, block, 0, stream>>>(pw);
+                else
+                    kf::kf_attn_prefill_wide_kernel<D, false, 2><<<grid, block, 0, stream>>>(pw);
+            } else if (mask) {
+                kf::kf_attn_prefill_wide_kernel<D, true, 1><<<grid, block, 0, stream>>>(pw);
+            } else {
+                kf::kf_attn_prefill_wide_kernel<D, false, 1><<<grid, block, 0, stream>>>(pw);
+            }
+            return hipGetLastError();
+        }
+        launch_prefill<D, 4>(pl, prm, mask, stream);
+    } else {
+        if constexpr (D == 64 || D == 128) {
+            if (pl.kv_groups == 4) {
+                launch_prefill<D, 8, 4>(pl, prm, mask, stream);
                 return hipGetLastError();
             }
-            launch_prefill<D, 4>(pl, prm, mask, stream);
-        } else {
-            if constexpr (D == 64 || D == 128) {
-                if (pl.kv_groups == 4) {
-                    launch_prefill<D, 8, 4>(pl, prm, mask, stream);
-                    return hipGetLastError();
-                }
-                if (pl.kv_groups == 2) {
-                    if (pl.waves == 8)
-                        launch_prefill<D, 8, 2>(pl, prm, mask, stream);
-                    else
-                        launch_prefill<D, 4, 2>(pl, prm, mask, stream);
-                    return hipGetLastError();
-                }
-            }
-            if constexpr (D == 64 || D == 128) {
-                // Two row blocks per wave: key counts give both one limit, so
-                // only causal calls stay on the 256-row kernel.
-                if (!prm.causal && pl.wide_row_tiles > 0) {
-                    kf::AttnParams pw = prm;
-                    pw.row_tiles = pl.wide_row_tiles;
-                    if (mask)
-                        kf::kf_attn_prefill_wide_kernel<D, true, 1><<<dim3(pl.wide_grid),
-                                                                      dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
-                    else
-                        kf::kf_attn_prefill_wide_kernel<D, false, 1><<<dim3(pl.wide_grid),
-                                                                       dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
-                    return hipGetLastError();
-                }
-            }
-            if (pl.waves == 8) {
-                launch_prefill<D, 8>(pl, prm, mask, stream);
-            } else if (pl.waves == 4) {
-                launch_prefill<D, 4>(pl, prm, mask, stream);
-            } else {
-                launch_prefill<D, 2>(pl, prm, mask, stream);
+            if (pl.kv_groups == 2) {
+                if (pl.waves == 8)
+                    launch_prefill<D, 8, 2>(pl, prm, mask, stream);
+                else
+                    launch_prefill<D, 4, 2>(pl, prm, mask, stream);
+                return hipGetLastError();
             }
         }
-        return hipGetLastError();
+        if constexpr (D == 64 || D == 128) {
+            // Two row blocks per wave: key counts give both one limit, so
+            // only causal calls stay on the 256-row kernel.
+            if (!prm.causal && pl.wide_row_tiles > 0) {
+                kf::AttnParams pw = prm;
+                pw.row_tiles = pl.wide_row_tiles;
+                if (mask)
+                    kf::kf_attn_prefill_wide_kernel<D, true, 1><<<dim3(pl.wide_grid),
+                                                                  dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
+                else
+                    kf::kf_attn_prefill_wide_kernel<D, false, 1><<<dim3(pl.wide_grid),
+                                                                   dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
+                return hipGetLastError();
+            }
+        }
+        if (pl.waves == 8) {
+            launch_prefill<D, 8>(pl, prm, mask, stream);
+        } else if (pl.waves == 4) {
+            launch_prefill<D, 4>(pl, prm, mask, stream);
+        } else {
+            launch_prefill<D, 2>(pl, prm, mask, stream);
+        }
     }
-    const dim3 grid(pl.grid), block(pl.threads);
-    if (prm.block_table) {
-        kf::kf_attn_decode_kernel<D, true><<<grid, block, 0, stream>>>(prm);
-    } else if (pl.short_stages == 0) {
-        kf::kf_attn_decode_kernel<D, false><<<grid, block, 0, stream>>>(prm);
-    } else if (pl.short_stages == 1) {
-        kf::kf_attn_decode_short_kernel<D, 1><<<grid, block, 0, stream>>>(prm);
-    } else {
-        if constexpr (kf::kShortMaxStages<D> >= 2)
-            kf::kf_attn_decode_short_kernel<D, 2><<<grid, block, 0, stream>>>(prm);
-        else
-            return hipErrorInvalidValue;  // the planner never asks for it
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || pl.path != KF_PATH_DECODE_SPLIT) return e;
+    return hipGetLastError();
+}
+
+// The split-merge kernel over the plan's partials (split decode and split
+// prefill).
+template <int D>
+hipError_t launch_merge(const Plan& pl, const kf::AttnParams& prm, hipStream_t stream) {
     const dim3 mgrid(pl.rows_total * ((D / 4) / pl.merge_cw)), mblock(kf::kMergeThreads);
     // The (column block, splits per lane) pairs merge_cols / merge_per_lane
     // produce: the widest block with up to kMergeTarget (kMergePer when the
@@ -413,6 +457,31 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
         return hipErrorInvalidValue;  // not a pair the planner makes
     }
     return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t stream) {
+    if (prefill_path(pl.path)) {
+        const hipError_t e = launch_prefill_kernel<D>(pl, prm, stream);
+        if (e != hipSuccess || pl.path != KF_PATH_PREFILL_SPLIT) return e;
+        return launch_merge<D>(pl, prm, stream);
+    }
+    const dim3 grid(pl.grid), block(pl.threads);
+    if (prm.block_table) {
+        kf::kf_attn_decode_kernel<D, true><<<grid, block, 0, stream>>>(prm);
+    } else if (pl.short_stages == 0) {
+        kf::kf_attn_decode_kernel<D, false><<<grid, block, 0, stream>>>(prm);
+    } else if (pl.short_stages == 1) {
+        kf::kf_attn_decode_short_kernel<D, 1><<<grid, block, 0, stream>>>(prm);
+    } else {
+        if constexpr (kf::kShortMaxStages<D> >= 2)
+            kf::kf_attn_decode_short_kernel<D, 2><<<grid, block, 0, stream>>>(prm);
+        else
+            return hipErrorInvalidValue;  // the planner never asks for it
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || pl.path != KF_PATH_DECODE_SPLIT) return e;
+    return launch_merge<D>(pl, prm, stream);
 }
 
 // Shared tail of kf_attn_fwd_ex and kf_attn_decode_paged: pointer and
@@ -482,7 +551,6 @@ int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const 
 // uses it in place of a caller workspace and never allocates.  In host code
 // `scratch` names a host-side stand-in, not device memory: only the address
 // hipGetSymbolAddress returns (kept per device) is passed to kernels.
-constexpr size_t kStaticScratchBytes = size_t(16) << 20;
 __device__ __align__(256) char scratch[kStaticScratchBytes];
 
 // Device address of this device's `scratch` (device current on the calling
@@ -541,7 +609,7 @@ int describe_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const 
     plan->grid_blocks = pl.wide_row_tiles > 0 ? pl.wide_grid : pl.grid;
     plan->block_threads = pl.wide_row_tiles > 0 ? kf::WideCfg<128>::kThreads : pl.threads;
     plan->workspace_bytes = pl.ws_bytes;
-    plan->splits_per_block = pl.path == KF_PATH_PREFILL ? 0 : pl.short_stages > 0 ? kf::kShortWaves : 1;
+    plan->splits_per_block = prefill_path(pl.path) ? 0 : pl.short_stages > 0 ? kf::kShortWaves : 1;
     return KF_OK;
 }
 
@@ -567,7 +635,7 @@ int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
     if (st != KF_OK) return st;
     char tmp[192];
     int n;
-    if (pl.path == KF_PATH_PREFILL) {
+    if (prefill_path(pl.path)) {
         const bool causal = (flags & KF_ATTN_CAUSAL) != 0;
         const bool mask = causal || kv_lens;
         if (pl.wide_row_tiles > 0 && (!causal || D >= 256))
@@ -576,6 +644,9 @@ int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
         else
             n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_kernel<%d, %s, %d, %d>", D,
                          mask ? "true" : "false", pl.waves, pl.kv_groups);
+        if (pl.path == KF_PATH_PREFILL_SPLIT)
+            n += snprintf(tmp + n, sizeof(tmp) - (size_t)n, " + kf_attn_split_merge_kernel<%d, %d, %d>", D,
+                          pl.merge_per, pl.merge_cw);
     } else {
         if (pl.short_stages > 0)
             n = snprintf(tmp, sizeof(tmp), "kf_attn_decode_short_kernel<%d, %d>", D, pl.short_stages);
@@ -620,7 +691,9 @@ int kf_attn_fwd_noalloc(const void* Q, const void* K, const void* V, void* O, fl
                         float* row_sumexp, int B, int q_len, int kv_len, int H_q, int H_kv, int D,
                         const int* kv_lens, int flags, void* stream) {
     Plan pl;
-    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), &pl);
+    // Split prefill partitions are limited to what the scratch holds.
+    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), &pl, false,
+                             kStaticScratchBytes);
     if (st != KF_OK) return st;
     if (pl.ws_bytes > kStaticScratchBytes) return KF_ERR_SCRATCH;
     void* ws = nullptr;
@@ -643,7 +716,7 @@ size_t kf_attn_decode_paged_workspace_bytes(int B, int q_len, int H_q, int H_kv,
     if (paged_geometry(page_size, max_pages_per_seq, 1, &sh, &cap) != KF_OK) return 0;
     Plan pl;
     if (make_plan(B, q_len, cap, H_q, H_kv, D, current_device_shape(), &pl, true) != KF_OK ||
-        pl.path == KF_PATH_PREFILL)
+        prefill_path(pl.path))
         return 0;
     return pl.ws_bytes;
 }
@@ -659,7 +732,7 @@ int kf_attn_decode_paged(const void* Q, const void* K_pages, const void* V_pages
     Plan pl;
     st = make_plan(B, q_len, cap, H_q, H_kv, D, current_device_shape(), &pl, true);
     if (st != KF_OK) return st;
-    if (pl.path == KF_PATH_PREFILL) return KF_ERR_SIZE;  // more than 32 query rows per KV head
+    if (prefill_path(pl.path)) return KF_ERR_SIZE;  // more than 32 query rows per KV head
     if (!block_table || !kv_lens) return KF_ERR_NULL;
     kf::AttnParams prm{};
     prm.kv_lens = kv_lens;

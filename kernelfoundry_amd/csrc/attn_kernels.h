@@ -93,8 +93,8 @@ struct AttnParams {
     int rows_per_group; // R = (H_q / H_kv) * q_len
     int kv_len;
     int row_tiles;      // prefill: ceil(R / rows per workgroup)
-    int n_splits;       // decode: KV partitions per group
-    int kv_per_split;   // decode: multiple of 32
+    int n_splits;       // KV partitions per group (split decode / split prefill), else 1
+    int kv_per_split;   // keys per partition: a multiple of 32 (of 32 x KV groups on prefill)
     int rows_total;     // B * H_q * q_len
     float scale;        // 1 / sqrt(D), fp32 (the reference's softmax scale)
     float scale_log2;   // scale * log2(e)
@@ -125,6 +125,8 @@ struct AttnParams {
 };
 
 enum : int { kOutF32 = 0, kOutF16 = 1, kOutBF16 = 2 };
+// Internal store target of the split prefill: fp32 partial O at p.Opart.
+constexpr int kOutPartial = 3;
 
 // fp32 -> bf16 bits, round to nearest even (inputs are finite).
 __device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
@@ -138,6 +140,8 @@ template <int kOut>
 __device__ __forceinline__ void store_out4_as(const AttnParams& p, size_t e, const f32x4& v) {
     if constexpr (kOut == kOutF32) {
         *reinterpret_cast<f32x4*>(p.O + e) = v;
+    } else if constexpr (kOut == kOutPartial) {
+        *reinterpret_cast<f32x4*>(p.Opart + e) = v;
     } else if constexpr (kOut == kOutF16) {
         const f16x4 h = __builtin_convertvector(v, f16x4);
         *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(p.O) + e) = h;
@@ -232,6 +236,15 @@ __device__ __forceinline__ f32x16 mfma32(const f16x8& a, const f16x8& b, const f
 }
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// exp2(m - rmax scale_log2): the factor that rebases a row's running sums
+// (kept relative to the exp2-domain offset m) to its true row max.  One
+// explicit fused multiply-add, so every kernel instantiation rounds it the
+// same way (left to contraction, the compiler fuses it in some and not in
+// others, and masked and unmasked results would differ in the last bit).
+__device__ __forceinline__ float rebase_factor(float m, float rmax, float scale_log2) {
+    return exp2_hw(__builtin_fmaf(-rmax, scale_log2, m));
+}
 
 // Cross-lane reductions on the VALU (no LDS round trip, unlike ds_bpermute):
 // v_permlane32_swap(x, x) yields the lower half's values in both halves and
@@ -771,13 +784,15 @@ __device__ __forceinline__ void block_update_max(RowState& st, float mx, float s
 // stores its own chunks,
 //   O = sum_g w_g O_g / L,  L = sum_g w_g l_g,  w_g = exp(m_g - max m),
 // summing over g = 0 .. KS-1 in that order whatever the owner, so the result
-// does not depend on which group stores a chunk.  Opens with the barrier
-// after which every group is done with its stage regions.
+// does not depend on which group stores a chunk.  With KV partitions
+// (p.n_splits > 1) the merged state goes to the split partials at index pi
+// instead (O unnormalised, m, L), for the split merge.  Opens with the
+// barrier after which every group is done with its stage regions.
 template <int D, int KS, int kRowWaves, class SlotBase>
 __device__ __forceinline__ void merge_kv_groups(const AttnParams& p, const RowState& st,
                                                 const f32x16 (&o)[D / 32], SlotBase slot_base,
                                                 float* merge_ml, int wave, int kgrp, int lane, int g,
-                                                size_t ri, bool row_ok) {
+                                                size_t ri, size_t pi, bool row_ok) {
     constexpr int kC = D / 32 * 4;                      // float4 chunks per lane
     constexpr int kCPer = kC / KS;                      // chunks each group stores
     static_assert(kC % KS == 0, "chunks per group");
@@ -793,7 +808,7 @@ __device__ __forceinline__ void merge_kv_groups(const AttnParams& p, const RowSt
     const float l_pair = sum_xor32(st.l);
     const bool none = st.rmax == -INFINITY;
     const float m_g = none ? -INFINITY : st.rmax * p.scale;
-    const float beta = none ? 0.f : exp2_hw(st.m - st.rmax * p.scale_log2);
+    const float beta = none ? 0.f : rebase_factor(st.m, st.rmax, p.scale_log2);
     __syncthreads();  // every group is done with its stage regions
     merge_ml[(kgrp * kRowWaves + wave) * 64 + lane] = m_g;
     merge_ml[((KS + kgrp) * kRowWaves + wave) * 64 + lane] = l_pair * beta;
@@ -814,7 +829,9 @@ __device__ __forceinline__ void merge_kv_groups(const AttnParams& p, const RowSt
         wgt[gg] = mo == -INFINITY ? 0.f : exp2_hw((mo - m_all) * kLog2e);
         L += wgt[gg] * merge_ml[((KS + gg) * kRowWaves + wave) * 64 + lane];
     }
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    const bool partial = p.n_splits > 1;
+    const float inv = partial ? 1.0f : L > 0.f ? 1.0f / L : 0.f;
+    const size_t oi = partial ? pi : ri;
     auto merge_store = [&](auto out) {
         constexpr int kOut = decltype(out)::value;
 #pragma unroll
@@ -827,16 +844,25 @@ __device__ __forceinline__ void merge_kv_groups(const AttnParams& p, const RowSt
                 acc = wgt[gg] * v + acc;
             }
             const int d = 32 * (cc / 4) + 8 * (cc % 4) + 4 * g;
-            if (row_ok && d < D) store_out4_as<kOut>(p, ri * D + d, acc * inv);
+            if (row_ok && d < D) store_out4_as<kOut>(p, oi * D + d, acc * inv);
         }
     };
-    if (p.out_dtype == kOutF16)
+    if (partial)
+        merge_store(std::integral_constant<int, kOutPartial>{});
+    else if (p.out_dtype == kOutF16)
         merge_store(std::integral_constant<int, kOutF16>{});
     else if (p.out_dtype == kOutBF16)
         merge_store(std::integral_constant<int, kOutBF16>{});
     else
         merge_store(std::integral_constant<int, kOutF32>{});
-    if (kgrp == 0 && row_ok && g == 0) store_stats(p, ri, m_all, L);
+    if (kgrp == 0 && row_ok && g == 0) {
+        if (partial) {
+            p.Mpart[pi] = m_all;
+            p.Lpart[pi] = L;
+        } else {
+            store_stats(p, ri, m_all, L);
+        }
+    }
 }
 
 // kMask: causal masking and/or per-sequence key counts (p.causal,
@@ -883,8 +909,15 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const int kgrp = KS == 1 ? 0 : wave_id / kRowWaves;        // KV group
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x, p.xcds);
-    int rt = blk % p.row_tiles;
-    const int grp = blk / p.row_tiles;
+    // KV partitions (p.n_splits > 1; the planner makes them at D <= 128
+    // only): workgroup blk takes partition blk % n_splits of its row tile's
+    // keys and writes split partials.
+    constexpr bool kSplits = D <= 128;
+    const int nsp = kSplits ? p.n_splits : 1;
+    const bool split_out = kSplits && nsp > 1;
+    const int split = blk % nsp;
+    int rt = blk / nsp % p.row_tiles;
+    const int grp = blk / nsp / p.row_tiles;
     const int R = p.rows_per_group;
     const int kv_len = p.kv_len;
     const float c = p.scale_log2;
@@ -927,20 +960,26 @@ void kf_attn_prefill_kernel(AttnParams p) {
             }
         }
     }
-    // KV group kgrp covers the keys [kv_base, kv_end) of the workgroup's
-    // range in tiles 0 .. ntiles - 1 (the same count for every group); row
-    // limits below are relative to kv_base.
-    const int ntiles_wg = (blk_lim + BC - 1) / BC;
+    // The workgroup's keys: [s0, blk_lim) (its partition of them when split).
+    // KV group kgrp covers [kv_base, kv_end) of them in tiles 0 .. ntiles - 1
+    // (the same count for every group); row limits below are relative to
+    // kv_base.
+    const int s0 = split * p.kv_per_split;
+    if (split_out) blk_lim = min(blk_lim, s0 + p.kv_per_split);
+    const int ntiles_wg = max(blk_lim - s0 + BC - 1, 0) / BC;
     const int ntiles = KS == 1 ? ntiles_wg : (ntiles_wg + KS - 1) / KS;  // 32-row tiles
     const int nstages = (ntiles * BC + SR - 1) / SR;                     // LDS stages
-    const int kv_base = kgrp * ntiles * BC;
+    const int kv_base = s0 + kgrp * ntiles * BC;
     const int kv_end = min(kv_base + ntiles * BC, blk_lim);
-    if constexpr (KS > 1) wave_min = min(wave_min, kv_end) - kv_base;
+    if (KS > 1 || kSplits) {
+        wave_min = min(wave_min, kv_end) - kv_base;
+        wave_max = min(wave_max, kv_end) - kv_base;
+    }
     // Tiles with a key visible to some row of this wave.  The later ones are
     // fully masked for it: their scores would contribute exactly nothing, so
     // the wave skips them and only takes part in the stage barriers and
     // copies (one KV group; with several, every group runs all its tiles).
-    const int nt_w = (kMask && KS == 1) ? min(ntiles, (wave_max + BC - 1) / BC) : ntiles;
+    const int nt_w = (kMask && KS == 1) ? min(ntiles, max(wave_max + BC - 1, 0) / BC) : ntiles;
     char* const b0 = buf0 + kgrp * S::kStageBytes;  // this group's stage regions
     char* const b1 = buf1 + kgrp * S::kStageBytes;
     char* const b2 = Cfg::kBuffers == 3 ? buf2 + kgrp * S::kStageBytes : buf2;  // unused at 2
@@ -1096,24 +1135,38 @@ void kf_attn_prefill_kernel(AttnParams p) {
 
     const int row = rt * kPrefillRows + wave * 32 + (lane & 31);
     if (kMask && ntiles == 0) {
-        // No key for any row of this workgroup (whole-workgroup uniform).
-        if (row < R) {
+        // No key for any row of this workgroup (whole-workgroup uniform):
+        // O = 0, Mi = -inf, Li = 0, or that partial (a partition the rows
+        // do not reach; the merge gives it weight 0 but reads it).
+        if (row < R && kgrp == 0) {
             const size_t ri = (size_t)grp * R + row;
+            const size_t pi = ((size_t)grp * nsp + split) * R + row;
 #pragma unroll
             for (int td = 0; td < kNTD; ++td)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int d = 32 * td + 8 * i + 4 * g;
-                    if (d < D) store_out4(p, ri * D + d, f32x4{0.f, 0.f, 0.f, 0.f});
+                    if (d >= D) continue;
+                    if (split_out)
+                        *reinterpret_cast<f32x4*>(p.Opart + pi * D + d) = f32x4{0.f, 0.f, 0.f, 0.f};
+                    else
+                        store_out4(p, ri * D + d, f32x4{0.f, 0.f, 0.f, 0.f});
                 }
-            if (g == 0) store_stats(p, ri, -INFINITY, 0.f);
+            if (g == 0) {
+                if (split_out) {
+                    p.Mpart[pi] = -INFINITY;
+                    p.Lpart[pi] = 0.f;
+                } else {
+                    store_stats(p, ri, -INFINITY, 0.f);
+                }
+            }
         }
         return;
     }
     // This lane's query row sees keys [0, lim_lane) (padding rows: blk_lim).
     int lim_lane = kv_len;
     if constexpr (kMask) lim_lane = row < R ? row_kv_limit(p, kvb, row % p.q_len) : blk_lim;
-    if constexpr (KS > 1) lim_lane = min(lim_lane, kv_end) - kv_base;
+    if (KS > 1 || kSplits) lim_lane = min(lim_lane, kv_end) - kv_base;
 
     // ---- Prologue: stage 0 and the K of stage 1 (two-buffer ring) or all of
     // stage 1 (three buffers) in flight, Q fragments, S(0). ----
@@ -1260,12 +1313,28 @@ void kf_attn_prefill_kernel(AttnParams p) {
         };
         __shared__ float merge_ml[2 * KS * kRowWaves * 64];
         merge_kv_groups<D, KS, kRowWaves>(p, st, o, slot_base, merge_ml, wave, kgrp, lane, g,
-                                          (size_t)grp * R + row, row < R);
+                                          (size_t)grp * R + row,
+                                          ((size_t)grp * nsp + split) * R + row, row < R);
         return;
     }
 
     // ---- Epilogue: combine the two half-row partial sums, normalise, store. ----
     const float l = sum_xor32(st.l);
+    if (split_out) {
+        // KV partition: the split partial, rebased to the true row max
+        // (O beta, l beta, m = rmax scale; a row without keys here: 0, 0, -inf).
+        const bool none = st.rmax == -INFINITY;
+        const float beta = none ? 0.f : rebase_factor(st.m, st.rmax, p.scale_log2);
+        if (row < R) {
+            const size_t pi = ((size_t)grp * nsp + split) * R + row;
+            store_o_row<kOutPartial, D>(p, pi, o, beta, g);
+            if (g == 0) {
+                p.Mpart[pi] = none ? -INFINITY : st.rmax * p.scale;
+                p.Lpart[pi] = l * beta;
+            }
+        }
+        return;
+    }
     const bool empty = kMask && !(l > 0.f);  // no visible key
     if (row < R) {
         const float inv = empty ? 0.f : 1.0f / l;
@@ -1273,7 +1342,7 @@ void kf_attn_prefill_kernel(AttnParams p) {
         store_o_row_any<D>(p, ri, o, inv, g);
         if (g == 0)
             store_stats(p, ri, st.rmax * p.scale,
-                        empty ? 0.f : l * exp2_hw(st.m - st.rmax * p.scale_log2));
+                        empty ? 0.f : l * rebase_factor(st.m, st.rmax, p.scale_log2));
     }
 }
 
@@ -1724,7 +1793,7 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
         auto slot_base = [&](int k) { return buf0 + k * 1024; };
         __shared__ float merge_ml[2 * KS * kRowWaves * 64];
         merge_kv_groups<D, KS, kRowWaves>(p, st0, o0, slot_base, merge_ml, wave, kgrp, lane, g,
-                                          (size_t)grp * R + row0, row0 < R);
+                                          (size_t)grp * R + row0, (size_t)grp * R + row0, row0 < R);
         return;
     }
 
@@ -1736,13 +1805,13 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
         store_o_row_any<D>(p, ri, o0, empty ? 0.f : 1.0f / l0, g);
         if (g == 0)
             store_stats(p, ri, st0.rmax * p.scale,
-                        empty ? 0.f : l0 * exp2_hw(st0.m - st0.rmax * p.scale_log2));
+                        empty ? 0.f : l0 * rebase_factor(st0.m, st0.rmax, p.scale_log2));
     }
     if (kRB == 2 && row1 < R) {
         const float l1 = sum_xor32(st1.l);
         const size_t ri = (size_t)grp * R + row1;
         store_o_row_any<D>(p, ri, o1, 1.0f / l1, g);
-        if (g == 0) store_stats(p, ri, st1.rmax * p.scale, l1 * exp2_hw(st1.m - st1.rmax * p.scale_log2));
+        if (g == 0) store_stats(p, ri, st1.rmax * p.scale, l1 * rebase_factor(st1.m, st1.rmax, p.scale_log2));
     }
 }
 
@@ -1939,7 +2008,7 @@ void kf_attn_decode_kernel(AttnParams p) {
     const float l_pair = sum_xor32(st.l);
     const bool empty = st.rmax == -INFINITY;
     const float m_nat = empty ? -INFINITY : st.rmax * p.scale;
-    const float beta = empty ? 0.f : exp2_hw(st.m - st.rmax * p.scale_log2);
+    const float beta = empty ? 0.f : rebase_factor(st.m, st.rmax, p.scale_log2);
 
     __syncthreads();  // all waves are done with their stage slots
     float* Ob = reinterpret_cast<float*>(smem_raw);

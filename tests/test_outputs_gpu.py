@@ -10,8 +10,8 @@ Mi + ln(Li) to 1e-3; rows without keys give LSE = -inf.
 
 Every kernel path that writes O is covered: prefill (unmasked and masked, the
 256-row and the wide kernel, masked by key counts and, at D = 256, causal;
-the KV-group merges of both kernels),
-decode without split (O written by the decode kernel), decode with split
+the KV-group merges of both kernels; the split prefill, whose O the merge
+kernel writes), decode without split (O written by the decode kernel), decode with split
 (O written by the merge kernel), and paged decode.
 """
 import numpy as np
@@ -49,6 +49,8 @@ CASES = [
     (1, 16, 4, 700, 500, 256, True, None),                # the same, causal, rows without keys
     (2, 16, 4, 300, 600, 256, False, [600, 31]),          # the same, key counts (one group without keys)
     (1, 8, 2, 128, 600, 128, False, None),                # prefill, four KV groups of 8 waves
+    (2, 32, 8, 64, 3000, 128, True, [3000, 0]),           # split prefill (merge kernel writes O)
+    (2, 32, 8, 40, 4096, 16, False, [4096, 100]),         # split prefill, one KV group per workgroup
     (2, 8, 8, 1, 100, 16, False, None),                   # decode, one split
     (2, 32, 8, 1, 3000, 128, True, [3000, 7]),            # decode + merge kernel
 ]

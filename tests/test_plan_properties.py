@@ -1,7 +1,7 @@
 """Property test of the dispatch planner (kf_attn_plan, host code only) over
 random shapes: every prefill plan's row tiles cover the query rows of a
-head, every decode plan covers all keys of a head exactly once with whole
-32-key stages, stays within the split merge's one-pass capacity, gives the
+head, every decode and split-prefill plan covers all keys of a head exactly
+once with whole 32-key stages, stays within the split merge's one-pass capacity, gives the
 streaming decode kernel at least one stage per wave in each split, and sizes
 the split workspace for every partial."""
 import pytest
@@ -41,6 +41,28 @@ def test_plan_invariants(B, H_kv, ratio, q, kv, D, cus):
         wide = (-(-R // 512),) if (waves == 8 and D in (64, 128)) else ()
         assert tiles in (-(-R // (32 * waves)), -(-R // (16 * waves)), -(-R // (8 * waves))) + wide
         assert p.workspace_bytes == 0 and p.num_splits == 1
+        return
+    if p.path == "prefill_split":
+        # The same workgroup layouts (D <= 128) with the keys split into
+        # partitions of whole tiles, only where the unsplit grid leaves half
+        # the CUs idle or more and the split grid fits one round; every key
+        # in exactly one partition; each KV group's serial chain at least 6
+        # tiles shorter; the partials sized.
+        assert R > 32 and D <= 128
+        waves = p.block_threads // 64
+        assert waves in (2, 4, 8)
+        assert p.grid_blocks % (n_groups * p.num_splits) == 0
+        tiles = p.grid_blocks // (n_groups * p.num_splits)
+        assert tiles in (-(-R // (32 * waves)), -(-R // (16 * waves)), -(-R // (8 * waves)))
+        assert 2 * n_groups * tiles <= cus and p.grid_blocks <= cus
+        assert 1 < p.num_splits <= 256 and p.kv_per_split % 32 == 0
+        # KV groups per workgroup (ks) consistent with the row tiles; the
+        # partition holds whole tiles of every group.
+        units = [32 * ks for ks in (1, 2, 4)
+                 if tiles == -(-R // (32 * waves // ks)) and p.kv_per_split % (32 * ks) == 0]
+        assert any(-(-kv // u) - p.kv_per_split // u >= 6 for u in units)
+        assert (p.num_splits - 1) * p.kv_per_split < kv <= p.num_splits * p.kv_per_split
+        assert p.workspace_bytes >= n_groups * p.num_splits * R * (D + 2) * 4
         return
     assert R <= 32
     assert p.kv_per_split % 32 == 0

@@ -68,7 +68,9 @@ def _both(torch, kf, B, H_q, H_kv, q, kv, D, seed, flags=0, lens=None):
     ((1, 32, 8, 1, 4096, 128, 0, None), (1, 32, 8, 1, 1000, 128, 0, None)),
     ((1, 32, 8, 4, 8192, 128, 1, [8000]), (2, 32, 8, 1, 3000, 128, 1, [3000, 77])),
     ((1, 32, 1, 1, 2048, 64, 0, None), (1, 16, 1, 1, 700, 64, 0, None)),
-], ids=["c2_then_smaller", "causal_lens_then_smaller", "mqa_then_smaller"])
+    ((1, 32, 8, 64, 4096, 128, 0, None), (1, 32, 8, 16, 2048, 128, 1, [1500])),
+], ids=["c2_then_smaller", "causal_lens_then_smaller", "mqa_then_smaller",
+        "split_prefill_then_smaller"])
 def test_noalloc_equals_workspace_entry_on_two_calls(first, second):
     import kernelfoundry_amd as kf
     torch = _torch()
