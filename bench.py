@@ -40,7 +40,11 @@ half of the metric):
                      and causal (visible-pair FLOPs), S = 512 / 1024 at
                      D=256 (small grids: two KV groups per workgroup), and
                      configs[2] with a per-sequence key count of 4000 (FLOPs
-                     over those keys).  Each line names its kernel.
+                     over those keys), and chunked prefill (q_len = 16 / 64 /
+                     128 / 256 query rows against 4096-16384 keys, 32 / 8 heads:
+                     the split prefill's KV partitions + split merge, the
+                     timed step covering both launches, spot-checked against
+                     the oracle).  Each line names its kernels.
 
 FLOPs = 4*B*H_q*q_len*kv_len*D and bytes = fp16 Q + unique fp16 K,V + fp32 O
 (tests/bench_flash_attn.cu:125-131).  ``roofline.achieved`` divides those by
@@ -672,6 +676,19 @@ def main():
     # configs[2] with a per-sequence key count (kf_attn_fwd_ex kv_lens): the
     # sequence uses its first 4000 of the 4096 allocated key rows.
     sweep.append(run_prefill(4096, key_count=4000))
+    # Chunked prefill (a short chunk of query rows against a long cache): the
+    # split prefill's KV partitions + split merge.
+    for q, kv in ((16, 8192), (64, 4096), (128, 8192), (256, 16384)):
+        cs = [_inputs(torch, 1, 32, 8, q, kv, 128, 77 + q + kv)]
+        rq = Runner(torch, kf, cs, 128)
+        ms, kern_mean, _ = time_steps(torch, rq, steps, warmup)
+        f = flops(1, 32, q, kv, 128)
+        sweep.append({"q_len": q, "kv_len": kv, "H_kv": 8, "D": 128, "ms": ms,
+                      "tflops": f / (ms * 1e9), "kernel_ms_mean": kern_mean,
+                      "grid_blocks": rq.plan.grid_blocks, "num_splits": rq.plan.num_splits,
+                      "kernels": kf.kernel_names(1, q, kv, 32, 8, 128),
+                      "parity": parity_spot_check(torch, rq, [(0, 0), (0, 31)])})
+        del rq
     # configs[3] decode: 0.54 MB per set, rotated over > 512 MB of distinct
     # sets like configs[1], so each step reads HBM, not the Infinity Cache.
     dq, _ = run_decode(1, 2048, 960, D=64, H_kv=1)

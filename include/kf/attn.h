@@ -115,7 +115,8 @@ int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
                          const int* kv_lens, char* buf, size_t buf_bytes);
 
 /* Bytes of device workspace kf_attn_fwd needs for this shape (0 when the
- * shape runs without split-KV partials).  Returns 0 for invalid shapes too;
+ * shape runs without split-KV partials: split decode and split prefill need
+ * them).  Returns 0 for invalid shapes too;
  * kf_attn_plan reports why. */
 size_t kf_attn_workspace_bytes(int B, int q_len, int kv_len, int H_q, int H_kv, int D);
 
@@ -173,7 +174,11 @@ int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, void* O,
  * process ends; the call makes no hipMalloc / hipFree or any other allocation.
  * Its address is resolved on the first call on each device (with that device
  * current on the calling thread).  A shape whose plan needs more than that
- * (kf_attn_workspace_bytes) returns KF_ERR_SCRATCH and launches nothing.
+ * (kf_attn_workspace_bytes) returns KF_ERR_SCRATCH and launches nothing,
+ * except a split prefill (KF_PATH_PREFILL_SPLIT), which is planned with as
+ * many KV partitions as the scratch holds -- possibly fewer than
+ * kf_attn_fwd_ex takes, in which case the results differ from its in the
+ * last bits (both within the same tolerance of the exact result).
  * Every call on one device shares that device's array: calls that can run
  * concurrently on one device (two streams, two threads) race on it and must
  * be serialised by the caller; consecutive calls on one stream are safe.  The
