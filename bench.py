@@ -41,7 +41,8 @@ half of the metric):
                      D=256 (small grids: two KV groups per workgroup), and
                      configs[2] with a per-sequence key count of 4000 (FLOPs
                      over those keys), and chunked prefill (q_len = 16 / 64 /
-                     128 / 256 query rows against 4096-16384 keys, 32 / 8 heads:
+                     128 / 256 query rows against 4096-16384 keys, 32 / 8 heads,
+                     D = 128, and 64 x 4096 at D = 256:
                      the split prefill's KV partitions + split merge, the
                      timed step covering both launches, spot-checked against
                      the oracle).  Each line names its kernels.
@@ -678,15 +679,16 @@ def main():
     sweep.append(run_prefill(4096, key_count=4000))
     # Chunked prefill (a short chunk of query rows against a long cache): the
     # split prefill's KV partitions + split merge.
-    for q, kv in ((16, 8192), (64, 4096), (128, 8192), (256, 16384)):
-        cs = [_inputs(torch, 1, 32, 8, q, kv, 128, 77 + q + kv)]
-        rq = Runner(torch, kf, cs, 128)
+    for q, kv, D in ((16, 8192, 128), (64, 4096, 128), (128, 8192, 128), (256, 16384, 128),
+                     (64, 4096, 256)):
+        cs = [_inputs(torch, 1, 32, 8, q, kv, D, 77 + q + kv)]
+        rq = Runner(torch, kf, cs, D)
         ms, kern_mean, _ = time_steps(torch, rq, steps, warmup)
-        f = flops(1, 32, q, kv, 128)
-        sweep.append({"q_len": q, "kv_len": kv, "H_kv": 8, "D": 128, "ms": ms,
+        f = flops(1, 32, q, kv, D)
+        sweep.append({"q_len": q, "kv_len": kv, "H_kv": 8, "D": D, "ms": ms,
                       "tflops": f / (ms * 1e9), "kernel_ms_mean": kern_mean,
                       "grid_blocks": rq.plan.grid_blocks, "num_splits": rq.plan.num_splits,
-                      "kernels": kf.kernel_names(1, q, kv, 32, 8, 128),
+                      "kernels": kf.kernel_names(1, q, kv, 32, 8, D),
                       "parity": parity_spot_check(torch, rq, [(0, 0), (0, 31)])})
         del rq
     # configs[3] decode: 0.54 MB per set, rotated over > 512 MB of distinct

@@ -62,6 +62,10 @@ constexpr int kMinSplitGroupKeys = 64;
 // Serial 32-key tiles per KV group a split prefill must save (measured at
 // 32 / 8 heads, D = 64 / 128: 4 saved tiles lose 3-22 %, 6 win 18-34 %).
 constexpr long long kMinSplitSavedTiles = 6;
+// Time of a 32-key tile of the 4-wave D = 256 prefill kernel (128 rows per
+// workgroup) relative to one of the wide kernel's KV groups (689 vs 487 us
+// for the whole S = 4096, 32 / 8 heads prefill).
+constexpr double kSplit256TileCost = 1.4;
 // kf_attn_fwd_noalloc's static scratch (split-KV partials), per device.
 constexpr size_t kStaticScratchBytes = size_t(16) << 20;
 // Time per query row of the wide prefill kernel relative to the 256-row
@@ -282,9 +286,11 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
         // kMinSplitGroupKeys keys of each partition (and the partials fit
         // ws_cap), and only where that shortens each KV group's serial chain
         // by kMinSplitSavedTiles 32-key tiles or more: the merge launch and
-        // the partials' round trip cost about that much.  D = 256 grids run
-        // the wide kernel's KV groups instead.
-        if (p.wide_row_tiles == 0 && D <= 128 && 2LL * p.grid <= cus) {
+        // the partials' round trip cost about that much.  At D = 256 the
+        // split runs the 4-wave kernel, whose 32-key tile costs
+        // kSplit256TileCost of a wide-kernel tile, against the wide kernel's
+        // chain (halved by its two KV groups where it has them).
+        if ((p.wide_row_tiles == 0 || D == 256) && 2LL * p.grid <= cus) {
             long long ns = cus / p.grid;
             const long long by_keys = kv_len / ((long long)ks * kMinSplitGroupKeys);
             if (ns > by_keys) ns = by_keys;
@@ -296,8 +302,15 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
                 long long per = (kv_len + ns - 1) / ns;
                 per = (per + unit - 1) / unit * unit;
                 ns = (kv_len + per - 1) / per;
-                const long long tiles = ((long long)kv_len + unit - 1) / unit;  // per KV group, unsplit
-                const long long saved = tiles - per / unit;
+                long long saved;
+                if (D == 256) {
+                    const long long wunit = 32LL * (p.wide_row_tiles > 0 ? p.wide_kv_groups : 1);
+                    const double chain = (double)((kv_len + wunit - 1) / wunit);
+                    saved = (long long)(chain - kSplit256TileCost * (double)(per / 32));
+                } else {
+                    const long long tiles = ((long long)kv_len + unit - 1) / unit;  // per KV group, unsplit
+                    saved = tiles - per / unit;
+                }
                 const int cw = kf::merge_cols(D, (int)ns);
                 if (ns > 1 && saved >= kMinSplitSavedTiles && (long long)p.grid * ns <= INT_MAX && rows_total * ((D / 4) / cw) <= INT_MAX) {
                     p.n_splits = (int)ns;
@@ -306,6 +319,8 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
                     p.merge_cw = cw;
                     p.merge_per = kf::merge_per_lane(cw, p.n_splits);
                     p.path = KF_PATH_PREFILL_SPLIT;
+                    p.wide_row_tiles = 0;  // D = 256: the 4-wave kernel
+                    p.wide_grid = 0;
                 }
             }
         }
@@ -330,6 +345,16 @@ int hip_fail(hipError_t e) {
 
 template <int D, int NW, int KS = 1>
 void launch_prefill(const Plan& pl, const kf::AttnParams& prm, bool mask, hipStream_t stream) {
+    if constexpr (D >= 256) {
+        // The KV-partition code is its own instantiation at D = 256.
+        if (pl.path == KF_PATH_PREFILL_SPLIT) {
+            if (mask)
+                kf::kf_attn_prefill_kernel<D, true, NW, KS, true><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+            else
+                kf::kf_attn_prefill_kernel<D, false, NW, KS, true><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+            return;
+        }
+    }
     if (mask)
         kf::kf_attn_prefill_kernel<D, true, NW, KS><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
     else

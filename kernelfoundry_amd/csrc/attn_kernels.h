@@ -875,7 +875,10 @@ __device__ __forceinline__ void merge_kv_groups(const AttnParams& p, const RowSt
 // same number of tiles (tiles past a group's keys are masked), so the
 // workgroup barriers line up.  At the end each group's (O, max, sum) is
 // rebased to its true max and group 0 merges them through LDS.
-template <int D, bool kMask, int NW = kPrefillMaxWaves<D>, int KS = 1>
+// kParts: the KV-partition code (split prefill) is compiled in; at D = 256
+// it is a separate instantiation, since its registers would push the
+// unsplit 4-wave kernel's past the architectural VGPRs.
+template <int D, bool kMask, int NW = kPrefillMaxWaves<D>, int KS = 1, bool kParts = (D <= 128)>
 __global__ __launch_bounds__((PrefillCfg<D, NW, KS>::kThreads), (PrefillCfg<D, NW, KS>::kWavesPerEU))
 void kf_attn_prefill_kernel(AttnParams p) {
     using Cfg = PrefillCfg<D, NW, KS>;
@@ -909,10 +912,9 @@ void kf_attn_prefill_kernel(AttnParams p) {
     const int kgrp = KS == 1 ? 0 : wave_id / kRowWaves;        // KV group
     const int g = lane >> 5;
     const int blk = xcd_remap(blockIdx.x, gridDim.x, p.xcds);
-    // KV partitions (p.n_splits > 1; the planner makes them at D <= 128
-    // only): workgroup blk takes partition blk % n_splits of its row tile's
-    // keys and writes split partials.
-    constexpr bool kSplits = D <= 128;
+    // KV partitions (p.n_splits > 1, kParts): workgroup blk takes partition
+    // blk % n_splits of its row tile's keys and writes split partials.
+    constexpr bool kSplits = kParts;
     const int nsp = kSplits ? p.n_splits : 1;
     const bool split_out = kSplits && nsp > 1;
     const int split = blk % nsp;

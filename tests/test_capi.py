@@ -48,7 +48,8 @@ def test_library_carries_gfx950_code():
 
 def test_no_kernel_uses_scratch(tmp_path):
     """Every kernel of the gfx950 code object keeps its state in registers and
-    LDS: no private (scratch) segment, no spilled VGPRs.  Read from the
+    LDS: no private (scratch) segment, no spilled VGPRs (but the AGPR spills
+    of one instantiation, below).  Read from the
     library's own code object metadata (llvm-objcopy + clang-offload-bundler
     + llvm-readelf from the ROCm toolchain)."""
     tools = "/opt/rocm/llvm/bin"
@@ -70,8 +71,15 @@ def test_no_kernel_uses_scratch(tmp_path):
         kernels[name] = (scratch, spills)
     assert any("kf_attn_prefill_kernel" in n for n in kernels)
     assert any("kf_attn_decode_kernel" in n for n in kernels)
-    bad = {n: v for n, v in kernels.items() if v != (0, 0)}
+    # One exception: the D = 256 prefill with its KV-partition code compiled
+    # in (kParts = true, the split prefill's instantiation) moves two values
+    # from VGPRs to AGPRs -- spills without a scratch segment, so no memory
+    # traffic (its unsplit instantiation has none).
+    split256 = re.compile(r"kf_attn_prefill_kernelILi256ELb[01]ELi4ELi1ELb1E")
+    bad = {n: v for n, v in kernels.items()
+           if v != (0, 0) and not (split256.search(n) and v[0] == 0 and v[1] <= 4)}
     assert not bad, f"kernels with scratch / spills: {bad}"
+    assert any(split256.search(n) for n in kernels)
 
 
 def test_version(lib):

@@ -6,10 +6,9 @@ by ~90 (e^-90 underflows the fp16 P to 0), so every output row must equal
 the last V row exactly, while every other V row holds -1; Mi must be that
 score and Li exactly 1.  A wrapped or truncated offset would read another
 row and show up as -1 / a wrong Mi.  Run through the decode kernels, the
-small-grid prefill and (65792 / 32896 query rows) the wide prefill kernel
-at D = 128 and 256, unmasked and masked (key count = kv_len), and (64 rows,
-D = 256) the wide kernel with two KV groups, whose second group starts at
-key kv_len / 2."""
+(65792 / 32896 query rows) the wide prefill kernel at D = 128 and 256, and
+(64 rows) the split prefill, whose last KV partition holds the last key,
+each unmasked and masked (key count = kv_len)."""
 import math
 
 import pytest
@@ -27,15 +26,18 @@ def test_last_key_at_the_offset_limit(q_len, H_q, D):
     names = kf.kernel_names(1, q_len, kv, H_q, 1, D)
     print("case", dict(q_len=q_len, H_q=H_q, D=D, kv=kv, path=kf.plan(1, q_len, kv, H_q, 1, D).path,
                        kernels=names), flush=True)
-    # 65792 / 32896 rows: the wide prefill kernel; 64 rows at D = 256: its
-    # KV-group form
-    wide = q_len > 1000 or (q_len == 64 and D == 256)
+    # 65792 / 32896 rows: the wide prefill kernel; 64 rows: the split prefill
+    wide = q_len > 1000
+    split = q_len == 64
+    masked = kf.kernel_names(1, q_len, kv, H_q, 1, D, masked=True)
     if wide:
-        ks = 1 if q_len > 1000 else 2
-        assert names == f"kf_attn_prefill_wide_kernel<{D}, false, {ks}>", names
+        assert names == f"kf_attn_prefill_wide_kernel<{D}, false, 1>", names
         # ... and its masked instantiation, with the key count set to kv_len
-        masked = kf.kernel_names(1, q_len, kv, H_q, 1, D, masked=True)
-        assert masked == f"kf_attn_prefill_wide_kernel<{D}, true, {ks}>", masked
+        assert masked == f"kf_attn_prefill_wide_kernel<{D}, true, 1>", masked
+    if split:
+        assert kf.plan(1, q_len, kv, H_q, 1, D).path == "prefill_split"
+        assert names.startswith(f"kf_attn_prefill_kernel<{D}, false, ") and "split_merge" in names
+        assert masked.startswith(f"kf_attn_prefill_kernel<{D}, true, ") and "split_merge" in masked
     dev = torch.device("cuda")
     K = torch.zeros((1, 1, kv, D), dtype=torch.float16, device=dev)
     V = torch.full((1, 1, kv, D), -1.0, dtype=torch.float16, device=dev)
@@ -44,7 +46,7 @@ def test_last_key_at_the_offset_limit(q_len, H_q, D):
     V[0, 0, -1] = vlast
     Q = torch.full((1, H_q, q_len, D), 0.5, dtype=torch.float16, device=dev)
     try:
-        runs = [None] + ([torch.tensor([kv], dtype=torch.int32, device=dev)] if wide else [])
+        runs = [None] + ([torch.tensor([kv], dtype=torch.int32, device=dev)] if wide or split else [])
         for lens in runs:
             O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True, kv_lens=lens)
             torch.cuda.synchronize()

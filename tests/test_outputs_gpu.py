@@ -51,6 +51,7 @@ CASES = [
     (1, 8, 2, 128, 600, 128, False, None),                # prefill, four KV groups of 8 waves
     (2, 32, 8, 64, 3000, 128, True, [3000, 0]),           # split prefill (merge kernel writes O)
     (2, 32, 8, 40, 4096, 16, False, [4096, 100]),         # split prefill, one KV group per workgroup
+    (2, 16, 4, 100, 3000, 256, True, None),               # split prefill at D=256 (4-wave kernel)
     (2, 8, 8, 1, 100, 16, False, None),                   # decode, one split
     (2, 32, 8, 1, 3000, 128, True, [3000, 7]),            # decode + merge kernel
 ]

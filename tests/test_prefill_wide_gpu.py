@@ -194,7 +194,7 @@ GROUP_CASES = [
     (1, 16, 4, 512, 512, False, None),                   # 16 tiles: 8 per group
     (1, 16, 4, 300, 333, False, None),                   # 11 tiles: group 1's last past the keys; padding rows
     (2, 8, 8, 256, 256, False, None),                    # MHA, 256 keys (the smallest KV-group case)
-    (1, 32, 1, 64, 1000, False, None),                   # MQA, 2048 rows, ragged keys
+    (1, 32, 1, 520, 1000, False, None),                  # MQA, 16640 rows (130 row tiles: no KV partitions), ragged keys
     (2, 16, 4, 257, 257, False, None),                   # 9 tiles, group 1 from key 160
     (1, 16, 4, 600, 600, True, None),                    # causal, ragged row tiles
     (1, 16, 4, 600, 777, True, None),                    # causal, kv_len > q_len
