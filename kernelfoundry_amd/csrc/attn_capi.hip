@@ -345,13 +345,13 @@ int hip_fail(hipError_t e) {
 
 template <int D, int NW, int KS = 1>
 void launch_prefill(const Plan& pl, const kf::AttnParams& prm, bool mask, hipStream_t stream) {
-    if constexpr (D >= 256) {
-        // The KV-partition code is its own instantiation at D = 256.
+    if constexpr (D >= 256 && NW == 4 && KS == 1) {
+        // The KV-partition code is a kernel of its own at D = 256.
         if (pl.path == KF_PATH_PREFILL_SPLIT) {
             if (mask)
-                kf::kf_attn_prefill_kernel<D, true, NW, KS, true><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+                kf::kf_attn_prefill_parts_kernel<D, true><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
             else
-                kf::kf_attn_prefill_kernel<D, false, NW, KS, true><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
+                kf::kf_attn_prefill_parts_kernel<D, false><<<dim3(pl.grid), dim3(pl.threads), 0, stream>>>(prm);
             return;
         }
     }
@@ -666,6 +666,8 @@ int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
         if (pl.wide_row_tiles > 0 && (!causal || D >= 256))
             n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d, %s, %d>", D, mask ? "true" : "false",
                          pl.wide_kv_groups);
+        else if (D >= 256 && pl.path == KF_PATH_PREFILL_SPLIT)
+            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_parts_kernel<%d, %s>", D, mask ? "true" : "false");
         else
             n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_kernel<%d, %s, %d, %d>", D,
                          mask ? "true" : "false", pl.waves, pl.kv_groups);

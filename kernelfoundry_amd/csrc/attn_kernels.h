@@ -875,12 +875,12 @@ __device__ __forceinline__ void merge_kv_groups(const AttnParams& p, const RowSt
 // same number of tiles (tiles past a group's keys are masked), so the
 // workgroup barriers line up.  At the end each group's (O, max, sum) is
 // rebased to its true max and group 0 merges them through LDS.
-// kParts: the KV-partition code (split prefill) is compiled in; at D = 256
-// it is a separate instantiation, since its registers would push the
-// unsplit 4-wave kernel's past the architectural VGPRs.
-template <int D, bool kMask, int NW = kPrefillMaxWaves<D>, int KS = 1, bool kParts = (D <= 128)>
-__global__ __launch_bounds__((PrefillCfg<D, NW, KS>::kThreads), (PrefillCfg<D, NW, KS>::kWavesPerEU))
-void kf_attn_prefill_kernel(AttnParams p) {
+// kParts: the KV-partition code (split prefill) is compiled in.  At D = 256
+// it is a kernel of its own (kf_attn_prefill_parts_kernel), since its
+// registers would push the unsplit 4-wave kernel's past the architectural
+// VGPRs.
+template <int D, bool kMask, int NW, int KS, bool kParts>
+__device__ __forceinline__ void prefill_body(AttnParams p) {
     using Cfg = PrefillCfg<D, NW, KS>;
     constexpr int BC = Cfg::BC;
     constexpr int kNSB = BC / 32;                 // 32-row score blocks per stage
@@ -1346,6 +1346,20 @@ void kf_attn_prefill_kernel(AttnParams p) {
             store_stats(p, ri, st.rmax * p.scale,
                         empty ? 0.f : l * rebase_factor(st.m, st.rmax, p.scale_log2));
     }
+}
+
+template <int D, bool kMask, int NW = kPrefillMaxWaves<D>, int KS = 1>
+__global__ __launch_bounds__((PrefillCfg<D, NW, KS>::kThreads), (PrefillCfg<D, NW, KS>::kWavesPerEU))
+void kf_attn_prefill_kernel(AttnParams p) {
+    prefill_body<D, kMask, NW, KS, (D <= 128)>(p);
+}
+
+// The split prefill at D = 256: the 4-wave kernel with KV partitions.
+template <int D, bool kMask>
+__global__ __launch_bounds__((PrefillCfg<D, 4, 1>::kThreads), (PrefillCfg<D, 4, 1>::kWavesPerEU))
+void kf_attn_prefill_parts_kernel(AttnParams p) {
+    static_assert(D == 256, "D <= 128 compiles the partitions into kf_attn_prefill_kernel");
+    prefill_body<D, kMask, 4, 1, true>(p);
 }
 
 // ---------------------------------------------------------------------------

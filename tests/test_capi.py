@@ -71,11 +71,11 @@ def test_no_kernel_uses_scratch(tmp_path):
         kernels[name] = (scratch, spills)
     assert any("kf_attn_prefill_kernel" in n for n in kernels)
     assert any("kf_attn_decode_kernel" in n for n in kernels)
-    # One exception: the D = 256 prefill with its KV-partition code compiled
-    # in (kParts = true, the split prefill's instantiation) moves two values
-    # from VGPRs to AGPRs -- spills without a scratch segment, so no memory
-    # traffic (its unsplit instantiation has none).
-    split256 = re.compile(r"kf_attn_prefill_kernelILi256ELb[01]ELi4ELi1ELb1E")
+    # One exception: the D = 256 split prefill (kf_attn_prefill_parts_kernel,
+    # the 4-wave kernel with its KV-partition code) moves two values from
+    # VGPRs to AGPRs -- spills without a scratch segment, so no memory
+    # traffic (the unsplit 4-wave kernel has none).
+    split256 = re.compile(r"kf_attn_prefill_parts_kernelILi256E")
     bad = {n: v for n, v in kernels.items()
            if v != (0, 0) and not (split256.search(n) and v[0] == 0 and v[1] <= 4)}
     assert not bad, f"kernels with scratch / spills: {bad}"

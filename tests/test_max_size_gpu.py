@@ -36,8 +36,9 @@ def test_last_key_at_the_offset_limit(q_len, H_q, D):
         assert masked == f"kf_attn_prefill_wide_kernel<{D}, true, 1>", masked
     if split:
         assert kf.plan(1, q_len, kv, H_q, 1, D).path == "prefill_split"
-        assert names.startswith(f"kf_attn_prefill_kernel<{D}, false, ") and "split_merge" in names
-        assert masked.startswith(f"kf_attn_prefill_kernel<{D}, true, ") and "split_merge" in masked
+        kern = "kf_attn_prefill_parts_kernel<256, " if D == 256 else f"kf_attn_prefill_kernel<{D}, "
+        assert names.startswith(kern + "false") and "split_merge" in names
+        assert masked.startswith(kern + "true") and "split_merge" in masked
     dev = torch.device("cuda")
     K = torch.zeros((1, 1, kv, D), dtype=torch.float16, device=dev)
     V = torch.full((1, 1, kv, D), -1.0, dtype=torch.float16, device=dev)
