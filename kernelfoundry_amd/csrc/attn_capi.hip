@@ -153,8 +153,9 @@ size_t split_ws_bytes(size_t parts, int D) {
 
 bool prefill_path(int path) { return path == KF_PATH_PREFILL || path == KF_PATH_PREFILL_SPLIT; }
 
-// ws_cap: most workspace the plan may ask for (split prefill only; the
-// split decode always fits kf_attn_fwd_noalloc's scratch).
+// ws_cap: most workspace a split prefill plan may ask for (it then takes
+// fewer KV partitions, or none); split decode plans ignore it, and
+// kf_attn_fwd_noalloc refuses those that exceed its scratch.
 int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const DeviceShape& dev,
               Plan* pl, bool paged = false, size_t ws_cap = SIZE_MAX) {
     const int cus = dev.cus;

@@ -111,3 +111,36 @@ def test_noalloc_refuses_a_shape_beyond_its_scratch():
     torch.cuda.synchronize()
     assert st == kf.KF_ERR_SCRATCH
     assert bool((O == 5.0).all())
+
+
+def test_noalloc_split_prefill_takes_the_partitions_its_scratch_holds():
+    """A split prefill whose full plan needs more partials than the static
+    scratch is planned with fewer KV partitions instead of being refused:
+    the call succeeds, allocates nothing, and agrees with the fp64 oracle
+    to the north-star bar on sampled heads and with kf_attn_fwd_ex (whose
+    plan has more partitions, so P is rounded to fp16 against other row
+    maxima) to 2e-4."""
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    lib = kf.load_library()
+    B, H_q, H_kv, q, kv, D = 1, 32, 8, 64, 4096, 256
+    assert kf.plan(B, q, kv, H_q, H_kv, D).path == "prefill_split"
+    assert kf.workspace_bytes(B, q, kv, H_q, H_kv, D) > lib.kf_attn_noalloc_scratch_bytes()
+    _announce(test="noalloc_split_prefill_capped", B=B, q=q, kv=kv, D=D)
+    Q, K, V = _inputs(torch, B, H_q, H_kv, q, kv, D, 11)
+    ref = kf.attn_fwd(Q, K, V)
+    O = torch.full((B, H_q, q, D), float("nan"), device="cuda")
+    st = lib.kf_attn_fwd_noalloc(Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(), None,
+                                 None, B, q, kv, H_q, H_kv, D, None, 0,
+                                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert st == kf.KF_OK, kf.status_string(st)
+    assert torch.isfinite(O).all()
+    assert (O - ref).abs().max().item() <= 2e-4
+    from oracle import attn_oracle as orc
+    q16, k16, v16 = (t.cpu().numpy() for t in (Q, K, V))
+    On = O.cpu().numpy()
+    for h in (0, 31):
+        want, _, _ = orc.sdpa(q16[:, h:h + 1], k16[:, h // 4:h // 4 + 1], v16[:, h // 4:h // 4 + 1])
+        ok, max_abs, rel = orc.within_tolerance(On[:, h:h + 1], want)
+        assert ok, (h, max_abs, rel)
