@@ -7,7 +7,8 @@ without the split merge, and the prefill kernel in every workgroup layout
 (8 waves x 256 rows, two KV groups of 8 or 4 waves, four KV groups of 8
 waves, 4 and 2 waves; D = 256 with 4 waves) and the wide prefill kernel (8
 waves x 64 rows at D = 64 / 128, 8 x 32 at D = 256, and at D = 256 its two
-KV groups of 4 waves), with causal masking, per-sequence key counts (empty
+KV groups of 4 waves), the split prefill (KV partitions + the split merge,
+at every head dimension), with causal masking, per-sequence key counts (empty
 sequences included), ragged lengths and every head dimension.  Each case is
 compared with oracle/attn_oracle.py's fp64 ``sdpa`` on the same fp16 inputs at
 the north-star bar (max |got - ref| <= 2e-3, ||got - ref|| / ||ref|| <= 1e-2;
@@ -70,6 +71,20 @@ def _cases(n=40, seed=2026):
     # form unmasked (random D = 256 shapes reach it masked).
     out.append((8, 32, 8, 150, 200, 256, True, None, 23))
     out.append((1, 8, 2, 200, 700, 256, False, None, 24))
+    # The split prefill (few query rows per KV head against many keys: KV
+    # partitions + the split merge), drawn from a second stream so the cases
+    # above stay as they are: every head dimension, masks and key counts.
+    rng2 = np.random.default_rng(seed + 1)
+    for i in range(8):
+        D = [16, 64, 128, 256][i % 4]
+        H_kv = int(rng2.choice([1, 2, 4, 8]))
+        H_q = H_kv * int(rng2.choice([4, 8]))
+        B = int(rng2.integers(1, 3))
+        q_len = int(rng2.integers(9, 65))
+        kv_len = int(rng2.integers(2000, 9000))
+        causal = bool(rng2.random() < 0.4)
+        kv_lens = [int(x) for x in rng2.integers(0, kv_len + 1, size=B)] if rng2.random() < 0.4 else None
+        out.append((B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens, int(rng2.integers(1 << 30))))
     return out
 
 
@@ -83,9 +98,15 @@ def _layout(kf, B, H_q, H_kv, q_len, kv_len, D, causal=False, masked=False):
     waves, kv_groups>), or ("prefill", "wide", kv_groups) for kf_attn_prefill_wide_kernel
     with either mask flag."""
     p = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
-    if p.path != "prefill":
+    if p.path not in ("prefill", "prefill_split"):
         return (p.path, f"short{p.kv_per_split}" if p.splits_per_block == 4 else "stream")
     name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, causal=causal, masked=masked)
+    if p.path == "prefill_split":
+        name = name.split(" + ")[0]
+        if name.startswith("kf_attn_prefill_parts_kernel"):
+            return ("prefill_split", "parts")
+        waves, groups = (int(x) for x in name.rstrip(">").split(",")[-2:])
+        return ("prefill_split", waves, groups)
     if name.startswith("kf_attn_prefill_wide"):  # the wide kernel, masked or not
         return ("prefill", "wide", int(name.rstrip(">").split(",")[-1]))
     waves, groups = (int(x) for x in name.rstrip(">").split(",")[-2:])
@@ -99,7 +120,8 @@ def test_sweep_covers_every_dispatch():
     want = {("decode", "short32"), ("decode_split", "short32"), ("decode_split", "short64"),
             ("decode", "stream"), ("decode_split", "stream"),
             ("prefill", 8, 1), ("prefill", 8, 2), ("prefill", 8, 4), ("prefill", 4, 2), ("prefill", 4, 1),
-            ("prefill", 2, 1), ("prefill", "wide", 1), ("prefill", "wide", 2)}
+            ("prefill", 2, 1), ("prefill", "wide", 1), ("prefill", "wide", 2),
+            ("prefill_split", 8, 4), ("prefill_split", 2, 1), ("prefill_split", "parts")}
     assert want <= seen, sorted(seen)
     # The split merge at its widest: 256 partials per row (4 columns per wave).
     assert any(kf.plan(c[0], c[3], c[4], c[1], c[2], c[5]).num_splits == 256 for c in CASES)
