@@ -367,7 +367,7 @@ int main() {
     for (const C& c : ref_cases)
         if (!run_case(c.B, c.S, c.S, c.H_q, c.H_kv, c.D, c.seed, true)) ++failed;
 
-    std::printf("[decode and mixed q_len/kv_len, asynchronous launcher with Mi/Li]\n");
+    std::printf("[decode, mixed q_len/kv_len and split prefill, asynchronous launcher with Mi/Li]\n");
     struct DC { int B, q_len, kv_len, H_q, H_kv, D; uint32_t seed; };
     const DC dec_cases[] = {
         {1, 1, 512, 32, 8, 128, 500},   {1, 1, 4096, 32, 8, 128, 501},
@@ -375,6 +375,9 @@ int main() {
         {2, 1, 1, 4, 2, 64, 504},       {1, 1, 33, 8, 1, 16, 505},
         {1, 1, 1000, 4, 4, 256, 506},   {3, 2, 777, 8, 2, 128, 507},
         {1, 16, 300, 8, 8, 64, 508},    {1, 40, 513, 16, 4, 128, 509},
+        // split prefill: few query rows per KV head against many keys
+        {1, 16, 4096, 32, 8, 128, 510}, {1, 32, 2048, 16, 4, 256, 511},
+        {2, 24, 3000, 16, 4, 64, 512},
     };
     for (const DC& c : dec_cases)
         if (!run_case(c.B, c.q_len, c.kv_len, c.H_q, c.H_kv, c.D, c.seed, false)) ++failed;
