@@ -128,7 +128,11 @@ size_t kf_attn_workspace_bytes(int B, int q_len, int kv_len, int H_q, int H_kv, 
  * (row_max / row_sumexp may be NULL), caller-owned workspace of at least
  * kf_attn_workspace_bytes() bytes (may be NULL when that is 0; 256-byte
  * aligned).  The workspace needs no initialisation; it must not be shared by
- * calls that can run concurrently (e.g. on two streams).
+ * calls that can run concurrently (e.g. on two streams).  Only split decode
+ * (KF_PATH_DECODE_SPLIT) requires it: a split prefill (KF_PATH_PREFILL_SPLIT)
+ * given no workspace, or a smaller one, runs with as many KV partitions as
+ * that workspace holds, or unsplit, instead of failing (its results then
+ * differ in the last bits, within the same tolerance).
  * Validation happens before any HIP call; an invalid argument returns its
  * status code and launches nothing.  Unlike launch_once, which silently
  * does nothing for an unsupported D (bench_flash_attn.cu:48-52), this
@@ -173,7 +177,11 @@ int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, void* O,
  * device, of kf_attn_noalloc_scratch_bytes() bytes (16 MiB), held until the
  * process ends; the call makes no hipMalloc / hipFree or any other allocation.
  * Its address is resolved on the first call on each device (with that device
- * current on the calling thread).  A shape whose plan needs more than that
+ * current on the calling thread) and kept for the life of the process; a
+ * hipDeviceReset() of that device unloads the array, so the call must not be
+ * used again on a device after resetting it.  Flag, pointer and alignment
+ * errors are reported as by kf_attn_fwd_ex, before any scratch check.  A
+ * shape whose plan needs more than that
  * (kf_attn_workspace_bytes) returns KF_ERR_SCRATCH and launches nothing,
  * except a split prefill (KF_PATH_PREFILL_SPLIT), which is planned with as
  * many KV partitions as the scratch holds -- possibly fewer than

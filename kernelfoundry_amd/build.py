@@ -16,7 +16,6 @@ REPO = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libkf_attn.so")
-PROBE_LIB_PATH = os.path.join(LIB_DIR, "libkf_probe.so")
 INCLUDE = os.path.join(REPO, "include")
 
 ARCH = "gfx950"
@@ -58,21 +57,8 @@ def build_library(verbose=False, extra_flags=()):
     return LIB_PATH
 
 
-def build_probe_library(verbose=False):
-    """libkf_probe.so: the measurement probes bench.py times beside the
-    decode (include/kf/probe.h)."""
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = PROBE_LIB_PATH + ".tmp"
-    cmd = [HIPCC, *DEVICE_FLAGS, "-shared", "-fPIC", f"-I{INCLUDE}",
-           os.path.join(CSRC, "probe.hip"), "-o", tmp]
-    run(cmd, verbose)
-    os.replace(tmp, PROBE_LIB_PATH)
-    return PROBE_LIB_PATH
-
-
 def build_all(verbose=False):
     build_library(verbose)
-    build_probe_library(verbose)
 
 
 if __name__ == "__main__":

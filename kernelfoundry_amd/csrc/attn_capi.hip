@@ -510,19 +510,30 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
     return launch_merge<D>(pl, prm, stream);
 }
 
-// Shared tail of kf_attn_fwd_ex and kf_attn_decode_paged: pointer and
-// workspace checks, the common kernel parameters, the launches.  `prm`
-// arrives with the masking / paging fields already set.
-int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const void* V, void* O,
-        float* row_max, float* row_sumexp, int q_len, int kv_len, int H_kv, int D, int flags,
-        void* workspace, size_t workspace_bytes, void* stream) {
+// Flag, pointer and alignment checks shared by every forward entry point,
+// in this order (after the shape checks of make_plan, before anything about
+// the workspace or scratch): unknown or conflicting flags, NULL tensors,
+// misaligned tensors, misaligned key-count / block-table arrays.
+int check_args(int flags, const void* Q, const void* K, const void* V, const void* O,
+               const int* kv_lens, const int* block_table) {
     constexpr int kKnown = KF_ATTN_CAUSAL | KF_ATTN_OUT_F16 | KF_ATTN_OUT_BF16 | KF_ATTN_LSE;
     if ((flags & ~kKnown) != 0) return KF_ERR_FLAGS;
     if ((flags & KF_ATTN_OUT_F16) && (flags & KF_ATTN_OUT_BF16)) return KF_ERR_FLAGS;
     if (!Q || !K || !V || !O) return KF_ERR_NULL;
     if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O)) return KF_ERR_ALIGN;
-    if ((reinterpret_cast<uintptr_t>(prm.kv_lens) & 3u) != 0) return KF_ERR_ALIGN;
-    if ((reinterpret_cast<uintptr_t>(prm.block_table) & 3u) != 0) return KF_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(kv_lens) & 3u) != 0) return KF_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(block_table) & 3u) != 0) return KF_ERR_ALIGN;
+    return KF_OK;
+}
+
+// Shared tail of kf_attn_fwd_ex and kf_attn_decode_paged: argument and
+// workspace checks, the common kernel parameters, the launches.  `prm`
+// arrives with the masking / paging fields already set.
+int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const void* V, void* O,
+        float* row_max, float* row_sumexp, int q_len, int kv_len, int H_kv, int D, int flags,
+        void* workspace, size_t workspace_bytes, void* stream) {
+    const int st = check_args(flags, Q, K, V, O, prm.kv_lens, prm.block_table);
+    if (st != KF_OK) return st;
     if (pl.ws_bytes > 0) {
         if (!workspace || workspace_bytes < pl.ws_bytes) return KF_ERR_WORKSPACE;
         if ((reinterpret_cast<uintptr_t>(workspace) & (kWsAlign - 1)) != 0) return KF_ERR_ALIGN;
@@ -580,7 +591,11 @@ int run(const Plan& pl, kf::AttnParams prm, const void* Q, const void* K, const 
 __device__ __align__(256) char scratch[kStaticScratchBytes];
 
 // Device address of this device's `scratch` (device current on the calling
-// thread), resolved once per device; nullptr and the HIP error on failure.
+// thread), resolved once per device and kept for the life of the process;
+// nullptr and the HIP error on failure.  hipDeviceReset() unloads this
+// library's code objects and with them the array, so the kept address is
+// stale after it: kf_attn_fwd_noalloc is not for processes that reset a
+// device they have already called it on.
 void* static_scratch(hipError_t* err) {
     static std::mutex mu;
     static void* addr[kMaxDevices] = {};
@@ -707,8 +722,16 @@ int kf_attn_fwd_ex(const void* Q, const void* K, const void* V, void* O, float* 
                    const int* kv_lens, int flags, void* workspace, size_t workspace_bytes,
                    void* stream) {
     Plan pl;
-    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), &pl);
+    const DeviceShape dev = current_device_shape();
+    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, dev, &pl);
     if (st != KF_OK) return st;
+    // A split prefill is an optimisation, not a requirement: without a
+    // workspace that holds its partials it runs with as many KV partitions
+    // as the given workspace holds, or unsplit (no workspace at all), so a
+    // prefill call never fails for want of a workspace.  Split decode plans
+    // keep their workspace requirement.
+    if (pl.path == KF_PATH_PREFILL_SPLIT && (!workspace || workspace_bytes < pl.ws_bytes))
+        (void)make_plan(B, q_len, kv_len, H_q, H_kv, D, dev, &pl, false, workspace ? workspace_bytes : 0);
     kf::AttnParams prm{};
     prm.kv_lens = kv_lens;
     return run(pl, prm, Q, K, V, O, row_max, row_sumexp, q_len, kv_len, H_kv, D, flags,
@@ -720,8 +743,11 @@ int kf_attn_fwd_noalloc(const void* Q, const void* K, const void* V, void* O, fl
                         const int* kv_lens, int flags, void* stream) {
     Plan pl;
     // Split prefill partitions are limited to what the scratch holds.
-    const int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), &pl, false,
-                             kStaticScratchBytes);
+    int st = make_plan(B, q_len, kv_len, H_q, H_kv, D, current_device_shape(), &pl, false,
+                       kStaticScratchBytes);
+    if (st != KF_OK) return st;
+    // The argument errors of kf_attn_fwd_ex come before any scratch question.
+    st = check_args(flags, Q, K, V, O, kv_lens, nullptr);
     if (st != KF_OK) return st;
     if (pl.ws_bytes > kStaticScratchBytes) return KF_ERR_SCRATCH;
     void* ws = nullptr;

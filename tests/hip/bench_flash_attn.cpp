@@ -15,10 +15,21 @@
 // launch_once (:39-54).  Like the reference, every iteration re-reads the
 // same K / V: the decode shapes here fit the 256 MB Infinity Cache, so their
 // GB/s are cache figures (bench.py rotates input sets for HBM figures).
+//
+// Options (for the profiling targets of tests/hip/CMakeLists.txt, which
+// profile one shape, as the reference's ncu targets profile one launch,
+// tests/CMakeLists.txt:23-33):
+//   --shape B,kv_len,H_q,H_kv,D[,q_len]   run that shape only (q_len 0 or
+//                                          absent: q_len = kv_len);
+//   --list   print every shape, one per line, as "B kv_len H_q H_kv D q_len
+//            kernels_per_launch" (2 on the split paths: kernel + merge) and
+//            exit without touching the GPU; rocprof_report.py uses it to
+//            cut a kernel trace of the whole bench into its shapes.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <random>
 #include <vector>
 
@@ -115,9 +126,27 @@ void bench(const Shape& s) {
 
 }  // namespace
 
-int main() {
-    std::printf("=== kernelfoundry_amd flash-attention benchmark, gfx950 (warmup=%d, iters=%d) ===\n",
-                kWarmup, kIters);
+int main(int argc, char** argv) {
+    bool list = false;
+    Shape only{};
+    bool have_only = false;
+    for (int i = 1; i < argc; ++i) {
+        if (std::strcmp(argv[i], "--list") == 0) {
+            list = true;
+        } else if (std::strcmp(argv[i], "--shape") == 0 && i + 1 < argc) {
+            only.q_len = 0;
+            const int n = std::sscanf(argv[++i], "%d,%d,%d,%d,%d,%d", &only.B, &only.kv_len, &only.H_q,
+                                      &only.H_kv, &only.D, &only.q_len);
+            if (n < 5) {
+                std::fprintf(stderr, "--shape wants B,kv_len,H_q,H_kv,D[,q_len]\n");
+                return EXIT_FAILURE;
+            }
+            have_only = true;
+        } else {
+            std::fprintf(stderr, "usage: %s [--list] [--shape B,kv_len,H_q,H_kv,D[,q_len]]\n", argv[0]);
+            return EXIT_FAILURE;
+        }
+    }
     struct Group {
         const char* title;
         std::vector<Shape> shapes;
@@ -138,6 +167,24 @@ int main() {
          {{1, 512, 32, 1, 128, 0}, {1, 1024, 32, 1, 128, 0}, {1, 512, 32, 1, 128, 1},
           {1, 1024, 32, 1, 128, 1}}},
     };
+    if (list) {
+        for (const Group& g : groups)
+            for (const Shape& s : g.shapes) {
+                const int q_len = s.q_len > 0 ? s.q_len : s.kv_len;
+                kf_attn_plan_t pl;
+                if (kf_attn_plan(s.B, q_len, s.kv_len, s.H_q, s.H_kv, s.D, &pl) != KF_OK) return EXIT_FAILURE;
+                const bool split = pl.path == KF_PATH_DECODE_SPLIT || pl.path == KF_PATH_PREFILL_SPLIT;
+                std::printf("%d %d %d %d %d %d %d\n", s.B, s.kv_len, s.H_q, s.H_kv, s.D, q_len, split ? 2 : 1);
+            }
+        return EXIT_SUCCESS;
+    }
+    std::printf("=== kernelfoundry_amd flash-attention benchmark, gfx950 (warmup=%d, iters=%d) ===\n",
+                kWarmup, kIters);
+    if (have_only) {
+        std::printf("\n[--shape]\n");
+        bench(only);
+        return EXIT_SUCCESS;
+    }
     for (const Group& g : groups) {
         std::printf("\n[%s]\n", g.title);
         for (const Shape& s : g.shapes) bench(s);

@@ -1,8 +1,11 @@
-"""Build the C++ HIP test/bench harness executables (test infrastructure).
+"""Build the C++ HIP test/bench harness executables and the measurement
+probes (test infrastructure).
 
-They link libkf_attn.so (rpath'd in-tree) and the oracle's C restatement of
-the reference's CPU attention (oracle/cpu_attn.c).  Outputs go to
-tests/hip/bin/, which travels to the GPU host with the tree.
+The executables link libkf_attn.so (rpath'd in-tree) and the oracle's C
+restatement of the reference's CPU attention (oracle/cpu_attn.c);
+libkf_probe.so (probe.hip, probe.h) holds the floors bench.py times beside the
+decode.  Outputs go to tests/hip/bin/, which travels to the GPU host with the
+tree.
 """
 from __future__ import annotations
 
@@ -17,6 +20,18 @@ if REPO not in sys.path:
 from kernelfoundry_amd import build as kbuild  # noqa: E402
 
 BIN = os.path.join(HERE, "bin")
+PROBE_LIB = os.path.join(BIN, "libkf_probe.so")
+
+
+def build_probe(verbose=False):
+    """libkf_probe.so: a bare read of the decode's K / V bytes and an empty
+    dispatch, timed by bench.py beside the decode step."""
+    os.makedirs(BIN, exist_ok=True)
+    cmd = [kbuild.HIPCC, *kbuild.DEVICE_FLAGS, "-shared", "-fPIC", f"-I{HERE}",
+           os.path.join(HERE, "probe.hip"), "-o", PROBE_LIB + ".tmp"]
+    kbuild.run(cmd, verbose)
+    os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
+    return PROBE_LIB
 
 
 def build(verbose=False):
@@ -37,6 +52,7 @@ def build(verbose=False):
         kbuild.run(cmd, verbose)
         os.replace(exe + ".tmp", exe)
         outs.append(exe)
+    outs.append(build_probe(verbose))
     return outs
 
 

@@ -1,5 +1,5 @@
 /*
- * kf/probe.h -- measurement probes of libkf_probe.so, used by bench.py to
+ * probe.h -- measurement probes of libkf_probe.so, used by bench.py to
  * put the floors of the small decode step beside its measured time.  Not part
  * of the attention ABI and no counterpart in the reference (whose bench,
  * tests/bench_flash_attn.cu:108-123, times only the kernel itself).

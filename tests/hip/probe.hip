@@ -1,5 +1,5 @@
 // probe.hip -- measurement probes of libkf_probe.so (used by bench.py; not
-// part of the attention ABI, declared in include/kf/probe.h).
+// part of the attention library or its ABI; declared in probe.h beside it).
 //
 // The decode of BASELINE configs[1] (B = 1, KV = 4096) moves 16.8 MB, which
 // HBM delivers in ~2 us: the step is bounded by what one kernel launch and
@@ -15,7 +15,7 @@
 
 #include <cstdint>
 
-#include "kf/probe.h"
+#include "probe.h"
 
 namespace {
 

@@ -444,13 +444,40 @@ def test_noalloc_validation(lib):
     assert lib.kf_attn_fwd_noalloc(FAKE, FAKE, FAKE, FAKE, None, None, 1, 300, 100, 8, 2, 128,
                                    None, 64, None) == kf.KF_ERR_FLAGS
     assert "static maximum" in kf.status_string(kf.KF_ERR_SCRATCH)
+    # On a shape beyond the scratch, argument errors still come first, as
+    # kf_attn_fwd_ex reports them: flags, NULL, misalignment, then SCRATCH.
+    assert lib.kf_attn_fwd_noalloc(*args, B, q, kv, H_q, H_kv, D, None, 64, None) == kf.KF_ERR_FLAGS
+    assert lib.kf_attn_fwd_noalloc(None, FAKE, FAKE, FAKE, None, None, B, q, kv, H_q, H_kv, D,
+                                   None, 0, None) == kf.KF_ERR_NULL
+    assert lib.kf_attn_fwd_noalloc(FAKE, FAKE + 2, FAKE, FAKE, None, None, B, q, kv, H_q, H_kv, D,
+                                   None, 0, None) == kf.KF_ERR_ALIGN
+    assert lib.kf_attn_fwd_noalloc(*args, B, q, kv, H_q, H_kv, D, ctypes.c_void_p(FAKE + 2), 0,
+                                   None) == kf.KF_ERR_ALIGN
+
+
+def test_split_prefill_runs_without_a_workspace(lib):
+    """A split prefill needs no workspace: given none (or too little) it is
+    re-planned with fewer KV partitions or unsplit, so the call gets past the
+    workspace check (on this GPU-less host it then fails at its first HIP
+    call), while a split decode still requires its workspace."""
+    shape = dict(B=1, q=16, kv=8192, H_q=32, H_kv=8, D=128)
+    assert kf.plan(1, 16, 8192, 32, 8, 128).path == "prefill_split"
+    need = kf.workspace_bytes(1, 16, 8192, 32, 8, 128)
+    assert need > 0
+    assert _fwd(**shape) == kf.KF_ERR_HIP
+    assert _fwd(ws=FAKE_WS, ws_bytes=need // 3, **shape) == kf.KF_ERR_HIP
+    assert _fwd(ws=FAKE_WS + 16, ws_bytes=need // 3, **shape) == kf.KF_ERR_ALIGN
+    assert _fwd(B=1, q=1, kv=4096, H_q=32, H_kv=8) == kf.KF_ERR_WORKSPACE
 
 
 def test_probe_library_exports_its_header():
-    """libkf_probe.so (bench.py's measurement probes) exports exactly what
-    include/kf/probe.h declares."""
-    lib_path = os.path.join(os.path.dirname(kf.LIB_PATH), "libkf_probe.so")
-    header = os.path.join(REPO, "include", "kf", "probe.h")
+    """libkf_probe.so (bench.py's measurement probes, built beside the C++
+    bench harness) exports exactly what tests/hip/probe.h declares, and the
+    product's library directory and public headers hold no probe."""
+    lib_path = os.path.join(REPO, "tests", "hip", "bin", "libkf_probe.so")
+    header = os.path.join(REPO, "tests", "hip", "probe.h")
+    assert not os.path.exists(os.path.join(os.path.dirname(kf.LIB_PATH), "libkf_probe.so"))
+    assert not os.path.exists(os.path.join(REPO, "include", "kf", "probe.h"))
     names = kf.exported_symbols(header)
     assert set(names) == {"kf_probe_read", "kf_probe_empty"}
     out = subprocess.run(["nm", "-D", "--defined-only", lib_path], capture_output=True,

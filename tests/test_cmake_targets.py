@@ -22,8 +22,23 @@ def test_cmake_harness_registers_test_and_profiling_targets(tmp_path):
         assert f"... {t}" in targets, targets
     if shutil.which("rocprofv3") or os.path.exists("/opt/rocm/bin/rocprofv3"):
         for t in ("rocprof_trace", "rocprof_mfma", "rocprof_bandwidth", "rocprof_stalls",
-                  "rocprof_latency"):
+                  "rocprof_latency", "rocprof_roofline", "rocprof_full"):
             assert f"... {t}" in targets, targets
+        # Like the reference's ncu targets (kernel name, the 5 warmup launches
+        # skipped: tests/CMakeLists.txt:23-33), every counter pass runs one
+        # shape under a kernel-name filter and the report skips the warmups.
+        for t in ("rocprof_mfma", "rocprof_bandwidth", "rocprof_stalls", "rocprof_latency",
+                  "rocprof_roofline"):
+            mk = (build / "CMakeFiles" / f"{t}.dir" / "build.make").read_text()
+            passes = [l for l in mk.splitlines() if "rocprofv3" in l and "--pmc" in l]
+            assert passes, t
+            for l in passes:
+                assert "--kernel-include-regex kf_attn_prefill_wide_kernel" in l, l
+                assert l.rstrip().endswith("bench_flash_attn --shape 1,4096,32,8,128"), l
+        mk = (build / "CMakeFiles" / "rocprof_trace.dir" / "build.make").read_text()
+        assert "rocprof_report.py trace" in mk and "shapes.md" in mk
+        mk = (build / "CMakeFiles" / "rocprof_full.dir" / "build.make").read_text()
+        assert "rocprof_report.py counters" in mk and "--skip 5 --count 50" in mk
     tests = subprocess.run(["ctest", "--test-dir", str(build), "-N"], check=True,
                            capture_output=True, text=True).stdout
     assert "flash_attn" in tests and "Total Tests: 1" in tests, tests
