@@ -37,8 +37,16 @@ def test_cmake_harness_registers_test_and_profiling_targets(tmp_path):
                 assert l.rstrip().endswith("bench_flash_attn --shape 1,4096,32,8,128"), l
         mk = (build / "CMakeFiles" / "rocprof_trace.dir" / "build.make").read_text()
         assert "rocprof_report.py trace" in mk and "shapes.md" in mk
+        # rocprof_full runs its six passes itself, one after another (the
+        # counters are device-wide: passes of a parallel build would mix).
         mk = (build / "CMakeFiles" / "rocprof_full.dir" / "build.make").read_text()
         assert "rocprof_report.py counters" in mk and "--skip 5 --count 50" in mk
+        passes = [l for l in mk.splitlines() if "rocprofv3" in l and "--pmc" in l]
+        assert [l.split(" -o ")[1].split()[0] for l in passes] == \
+            ["mfma", "fetch", "write", "stalls", "latency", "roofline"]
+        deps = (build / "CMakeFiles" / "Makefile2").read_text()
+        full_deps = [l for l in deps.splitlines() if l.startswith("CMakeFiles/rocprof_full.dir/all:")]
+        assert full_deps and not any("rocprof_mfma" in l or "rocprof_stalls" in l for l in full_deps)
     tests = subprocess.run(["ctest", "--test-dir", str(build), "-N"], check=True,
                            capture_output=True, text=True).stdout
     assert "flash_attn" in tests and "Total Tests: 1" in tests, tests
