@@ -29,7 +29,9 @@ half of the metric):
                      (kf_attn_decode_paged): 16-row pages scattered over a
                      pool twice the needed size (the reference's worst-case
                      fragmentation, bench_flash_attn2.py:153-215); bytes =
-                     configs[4]'s plus the block table.
+                     configs[4]'s plus the block table.  ``decode_paged_c1``:
+                     the configs[1] decode over such a cache (rotated over
+                     > 512 MB of pools).
   * ``decode_sweep`` -- the reference bench's decode shapes (B=1 KV=512..4096,
                      B=8 KV=512/1024, MQA KV=512/1024; tests/bench_flash_attn.cu:
                      154-159, 181-182), each rotated over > 512 MB of sets,
@@ -308,49 +310,66 @@ def parity_spot_check(torch, runner, heads, causal=False):
 
 
 def run_paged_decode(torch, kf, steps, warmup, check, B=32, kv=8192, H_q=32, H_kv=8, D=128,
-                     page_size=16):
-    """configs[4] decode over a fragmented paged cache; returns a result dict."""
+                     page_size=16, label="configs[4]"):
+    """A decode over a fragmented paged cache: each set's pages are randomly
+    placed in a pool twice the needed size; sets (pools, tables, queries) are
+    rotated through until they exceed the Infinity Cache.  Returns a result
+    dict."""
     max_pages = kv // page_size
     num_pages = 2 * B * max_pages
+    set_bytes = 2 * num_pages * H_kv * page_size * D * 2
+    n_sets = int(max(1, min(64, math.ceil(ROTATE_BYTES / set_bytes))))
     g = torch.Generator(device="cuda")
     g.manual_seed(4242)
-    Kp = torch.randn((num_pages, H_kv, page_size, D), generator=g, device="cuda").half()
-    Vp = torch.randn((num_pages, H_kv, page_size, D), generator=g, device="cuda").half()
-    Q = torch.randn((B, H_q, 1, D), generator=g, device="cuda").half()
-    table = torch.randperm(num_pages, generator=g, device="cuda")[:B * max_pages] \
-        .to(torch.int32).reshape(B, max_pages).contiguous()
+    sets = []
+    for _ in range(n_sets):
+        Kp = torch.randn((num_pages, H_kv, page_size, D), generator=g, device="cuda").half()
+        Vp = torch.randn((num_pages, H_kv, page_size, D), generator=g, device="cuda").half()
+        Q = torch.randn((B, H_q, 1, D), generator=g, device="cuda").half()
+        table = torch.randperm(num_pages, generator=g, device="cuda")[:B * max_pages] \
+            .to(torch.int32).reshape(B, max_pages).contiguous()
+        O = torch.empty((B, H_q, 1, D), dtype=torch.float32, device="cuda")
+        sets.append((Q, Kp, Vp, table, O))
     lens = torch.full((B,), kv, dtype=torch.int32, device="cuda")
-    O = torch.empty((B, H_q, 1, D), dtype=torch.float32, device="cuda")
     need = kf.paged_workspace_bytes(B, 1, H_q, H_kv, D, page_size, max_pages)
     ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
     lib = kf.load_library()
     stream = torch.cuda.current_stream()
-    args = (Q.data_ptr(), Kp.data_ptr(), Vp.data_ptr(), table.data_ptr(), lens.data_ptr(),
-            O.data_ptr(), None, None, B, 1, H_q, H_kv, D, page_size, max_pages, num_pages, 0,
-            ws.data_ptr(), need, stream.cuda_stream)
+    args = [(Q.data_ptr(), Kp.data_ptr(), Vp.data_ptr(), table.data_ptr(), lens.data_ptr(),
+             O.data_ptr(), None, None, B, 1, H_q, H_kv, D, page_size, max_pages, num_pages, 0,
+             ws.data_ptr(), need, stream.cuda_stream) for (Q, Kp, Vp, table, O) in sets]
 
     class _R:
         stream = None
+        i = 0
 
         def launch(self):
-            st = lib.kf_attn_decode_paged(*args)
+            a = args[self.i % n_sets]
+            self.i += 1
+            st = lib.kf_attn_decode_paged(*a)
             if st != 0:
                 raise RuntimeError(f"kf_attn_decode_paged failed: {kf.status_string(st)}")
 
     r = _R()
     r.stream = stream
     ms, kern_mean, _ = time_steps(torch, r, steps, warmup, PASSES)
-    by = nbytes(B, H_q, H_kv, 1, kv, D) + table.numel() * 4
-    out = {"config": f"configs[4] over a paged cache: B={B} KV={kv} page_size={page_size}, "
+    by = nbytes(B, H_q, H_kv, 1, kv, D) + B * max_pages * 4
+    # The paged forms of the kernels the contiguous plan names.
+    kern = kf.kernel_names(B, 1, kv, H_q, H_kv, D).replace(
+        "decode_short_kernel", "decode_short_paged_kernel").replace(
+        "kf_attn_decode_kernel<%d, false>" % D, "kf_attn_decode_kernel<%d, true>" % D)
+    out = {"config": f"{label} over a paged cache: B={B} KV={kv} page_size={page_size}, "
                      f"pages randomly placed in a {num_pages}-page pool",
            "latency_us": round(ms * 1e3, 2), "hbm_gbs": round(by / (ms * 1e6), 1),
            "launch_us_mean": round(kern_mean * 1e3, 2), "bytes_per_launch": by,
+           "sets_rotated": n_sets, "passes": PASSES, "kernels": kern,
            "roofline": {"bound": "hbm", "achieved": round(by / (ms * 1e6), 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s",
                         "frac": round(by / (ms * 1e6) / PEAK_HBM_GBS, 4)}}
     if check:
         from oracle import attn_oracle as orc
         import numpy as np
+        Q, Kp, Vp, table, O = sets[(r.i - 1) % n_sets]
         tb = table.cpu().numpy()
         heads = [(0, 0), (B - 1, H_q - 1)]
         worst = (0.0, 0.0)
@@ -366,6 +385,8 @@ def run_paged_decode(torch, kf, steps, warmup, check, B=32, kv=8192, H_q=32, H_k
             worst = (max(worst[0], mx), max(worst[1], rel))
         out["parity"] = {"heads": [list(x) for x in heads], "max_abs": worst[0],
                          "rel_l2": worst[1], "atol": orc.ATOL, "rtol": orc.RTOL, "ok": True}
+    del sets, args
+    torch.cuda.empty_cache()
     return out
 
 
@@ -697,6 +718,9 @@ def main():
         results["decode_paged"] = run_paged_decode(torch, kf, steps, warmup, args.only is None)
         if args.only:
             return
+        print("bench: paged decode B=1 KV=4096 page 16", file=sys.stderr, flush=True)
+        results["decode_paged_c1"] = run_paged_decode(torch, kf, steps, warmup, True, B=1, kv=4096,
+                                                      label="configs[1]")
 
     print("bench: decode sweep", file=sys.stderr, flush=True)
     probe = load_probe(kf)
@@ -858,6 +882,7 @@ def main():
             "parity": b32["parity"],
         },
         "decode_paged": results["decode_paged"],
+        "decode_paged_c1": results["decode_paged_c1"],
         "decode_sweep": decode_sweep,
         "sweep": sweep,
         "parity": pre.get("parity"),

@@ -143,8 +143,9 @@ struct Plan {
     int xcds;           // XCDs of the target device (workgroup id remap)
 };
 
-// paged: K/V come from a page pool (kf_attn_decode_paged), which only the
-// streaming decode kernel reads.  cus: compute units of the target device.
+// paged: K/V come from a page pool (kf_attn_decode_paged); the planner
+// makes the same choice as for a contiguous cache (both decode kernels have
+// a paged form).  cus: compute units of the target device.
 // Workspace bytes of split partials (O, M, L) for `parts` (partition, row)
 // pairs.
 size_t split_ws_bytes(size_t parts, int D) {
@@ -178,9 +179,10 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
     if (R <= kDecodeMaxRows) {
         // Short splits (one wave each) while the whole job is a few waves
         // per CU: 64 keys per split (D <= 128) while that keeps 4 waves per
-        // CU, else 32, else 64.
+        // CU, else 32, else 64.  Paged caches too (pages of >= 16 rows: a
+        // split spans at most 4 pages).
         int nst = 0;
-        if (!paged) {
+        {
             const auto waves = [&](int st) { return n_groups * ((kv_len + 32LL * st - 1) / (32LL * st)); };
             const auto fits = [&](int st) {
                 return st <= (D >= 256 ? 1 : 2) && waves(st) <= kShortMaxWavesPerCU * cus &&
@@ -494,7 +496,16 @@ hipError_t launch_all(const Plan& pl, const kf::AttnParams& prm, hipStream_t str
     }
     const dim3 grid(pl.grid), block(pl.threads);
     if (prm.block_table) {
-        kf::kf_attn_decode_kernel<D, true><<<grid, block, 0, stream>>>(prm);
+        if (pl.short_stages == 0) {
+            kf::kf_attn_decode_kernel<D, true><<<grid, block, 0, stream>>>(prm);
+        } else if (pl.short_stages == 1) {
+            kf::kf_attn_decode_short_paged_kernel<D, 1><<<grid, block, 0, stream>>>(prm);
+        } else {
+            if constexpr (kf::kShortMaxStages<D> >= 2)
+                kf::kf_attn_decode_short_paged_kernel<D, 2><<<grid, block, 0, stream>>>(prm);
+            else
+                return hipErrorInvalidValue;  // the planner never asks for it
+        }
     } else if (pl.short_stages == 0) {
         kf::kf_attn_decode_kernel<D, false><<<grid, block, 0, stream>>>(prm);
     } else if (pl.short_stages == 1) {

@@ -18,10 +18,11 @@
 //                              a workgroup merge in LDS; with several splits
 //                              each workgroup writes an unnormalised partial;
 //                              kPaged reads K/V through a block table.
-//   kf_attn_decode_short_kernel<D, NST>
+//   kf_attn_decode_short_kernel<D, NST> / kf_attn_decode_short_paged_kernel<D, NST>
 //                              split-KV for small decode jobs: every wave is
 //                              one split of 32 or 64 keys and issues all of
-//                              its loads at once (one memory round trip).
+//                              its loads at once (one memory round trip);
+//                              the paged form reads K/V through a block table.
 //   kf_attn_split_merge_kernel<D, NPER, CW>
 //                              merges the split partials into O, Mi, Li.
 //
@@ -2106,26 +2107,37 @@ void kf_attn_decode_kernel(AttnParams p) {
 // are in registers at once, so the softmax uses their exact maximum (no
 // running rescale).  The wave writes its partial (O unnormalised, M, l) or,
 // with one split, the final row; no workgroup barrier anywhere.
+//
+// kPaged (kf_attn_decode_short_paged_kernel): K / V are page pools read
+// through p.block_table.  Pages hold >= 16 rows, so a split of <= 64 keys
+// spans at most 4 pages; the wave reads their ids with wave-uniform (scalar)
+// loads before its K / V loads and each lane addresses its rows through
+// them.  A row on a page id outside [0, num_pages) is loaded from page 0
+// instead (the invalid page is never read), its scores are masked to -inf
+// and its V row is zeroed in the slot, so it contributes exactly nothing.
 // ---------------------------------------------------------------------------
 constexpr int kShortWaves = 4;  // waves (independent splits) per workgroup
 
 template <int D> constexpr int kShortMaxStages = D >= 256 ? 1 : 2;
 
-template <int D, int NST>
-__global__ __launch_bounds__(64 * kShortWaves, D >= 256 ? 1 : 2)
-void kf_attn_decode_short_kernel(AttnParams p) {
+template <int D, int NST> struct ShortCfg {
+    static constexpr int kKeys = 32 * NST;                // keys per split
+    static constexpr int kVBytes = kKeys * D * 2;         // V slot per wave
+};
+
+template <int D, int NST, bool kPaged>
+__device__ __forceinline__ void decode_short_body(const AttnParams& p, char* vbuf) {
     static_assert(NST >= 1 && NST <= kShortMaxStages<D>, "stages per split");
     constexpr int kRowBytes = D * 2;
     constexpr int kChunks = D / 8;                   // 16-byte chunks per row
-    constexpr int kKeys = 32 * NST;                  // keys per split
-    constexpr int kVBytes = kKeys * kRowBytes;       // V slot per wave
+    constexpr int kKeys = ShortCfg<D, NST>::kKeys;   // keys per split
+    constexpr int kVBytes = ShortCfg<D, NST>::kVBytes;
     constexpr int kRowsPerInstr = 1024 / kRowBytes;  // rows per LDS-DMA instruction
     constexpr int kInstr = kVBytes / 1024;
     constexpr int kNKK = D / 16;                     // MFMA k-steps over D
     constexpr int kNTD = (D < 32 ? 32 : D) / 32;     // 32-row O^T tiles
     static_assert(kVBytes % 1024 == 0, "V slot in whole KiB");
     using SW = SwizzleRow<D>;
-    __shared__ __attribute__((aligned(1024))) char vbuf[kShortWaves * kVBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -2175,8 +2187,36 @@ void kf_attn_decode_short_kernel(AttnParams p) {
     // below. ----
     const int last = s1 - 1;
     const uint16_t* Qg = p.Q + (size_t)grp * R * D;
-    const uint16_t* Kh = p.K + (size_t)grp * p.kv_len * D;
-    const char* Vh = reinterpret_cast<const char*>(p.V + (size_t)grp * p.kv_len * D);
+    const uint16_t* Kh = kPaged ? p.K : p.K + (size_t)grp * p.kv_len * D;
+    const char* Vh = reinterpret_cast<const char*>(kPaged ? p.V : p.V + (size_t)grp * p.kv_len * D);
+    // Paged: the ids of the (at most 4) pages of keys [s0, last], the first
+    // one pg0; an invalid id reads page 0 and flags its keys (bad_pages bit j).
+    int pid[4] = {0, 0, 0, 0};
+    int pg0 = 0, bad_pages = 0, hkv = 0;
+    if constexpr (kPaged) {
+        const int* tbl = p.block_table + (size_t)(grp / p.heads_kv) * p.max_pages;
+        hkv = grp % p.heads_kv;
+        pg0 = s0 >> p.page_shift;
+        const int pgl = last >> p.page_shift;  // pgl - pg0 <= 3
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int id = tbl[min(pg0 + j, pgl)];
+            const bool ok = (unsigned)id < (unsigned)p.num_pages;
+            pid[j] = ok ? id : 0;
+            if (!ok && pg0 + j <= pgl) bad_pages |= 1 << j;
+        }
+    }
+    // Element offset of key row kv (s0 <= kv <= last) in K / V.
+    auto row_off = [&](int kv) -> size_t {
+        if constexpr (kPaged) {
+            const int j = (kv >> p.page_shift) - pg0;
+            const int id = j == 0 ? pid[0] : j == 1 ? pid[1] : j == 2 ? pid[2] : pid[3];
+            return ((((size_t)id * p.heads_kv + hkv) << p.page_shift) +
+                    (size_t)(kv & ((1 << p.page_shift) - 1))) * D;
+        } else {
+            return (size_t)kv * D;
+        }
+    };
     // Lane l of DMA instruction ii writes LDS bytes [16 l, 16 l + 16) of KiB ii
     // of the slot: row r = ii * kRowsPerInstr + l / kChunks, physical chunk
     // l % kChunks, which holds logical chunk (l % kChunks) ^ h(r) of key s0 + r.
@@ -2185,9 +2225,13 @@ void kf_attn_decode_short_kernel(AttnParams p) {
     for (int ii = 0; ii < kInstr; ++ii) {
         const int r = ii * kRowsPerInstr + lane / kChunks;
         const int kv = min(s0 + r, last);
-        const uint32_t off = (uint32_t)kv * kRowBytes +
-                             (uint32_t)((((lane % kChunks) ^ SW::h(r)) % kChunks) * 16);
-        __builtin_amdgcn_global_load_lds(Vh + off, (lds_void*)(vs + ii * 1024), 16, 0, 0);
+        const uint32_t chunk = (uint32_t)((((lane % kChunks) ^ SW::h(r)) % kChunks) * 16);
+        const char* src;
+        if constexpr (kPaged)
+            src = Vh + row_off(kv) * 2 + chunk;
+        else
+            src = Vh + ((uint32_t)kv * kRowBytes + chunk);
+        __builtin_amdgcn_global_load_lds(src, (lds_void*)(vs + ii * 1024), 16, 0, 0);
     }
     f16x8 qf[kNKK];
     load_q_frags<D>(Qg, row, R, lane, qf);
@@ -2195,9 +2239,10 @@ void kf_attn_decode_short_kernel(AttnParams p) {
 #pragma unroll
     for (int b = 0; b < NST; ++b) {
         const int kv = min(s0 + 32 * b + row, last);
+        const uint16_t* kr = Kh + row_off(kv);
 #pragma unroll
         for (int kk = 0; kk < kNKK; ++kk)
-            kf[b][kk] = *reinterpret_cast<const f16x8*>(Kh + (size_t)kv * D + (2 * kk + g) * 8);
+            kf[b][kk] = *reinterpret_cast<const f16x8*>(kr + (2 * kk + g) * 8);
     }
     __builtin_amdgcn_sched_barrier(0);  // no MFMA (and its wait) above the loads
 
@@ -2213,6 +2258,18 @@ void kf_attn_decode_short_kernel(AttnParams p) {
     if (s0 + kKeys > min(s1, lim_min)) {
         const int lim_lane = row < R ? row_kv_limit(p, kvb, row % p.q_len) : kvb;
         block_mask<NST>(s, min(s1, lim_lane) - s0, lane);
+    }
+    // Keys on an invalid page (paged, wave-uniform branch): score -inf.
+    auto bad_key = [&](int k) {  // key s0 + k, 0 <= k < kKeys (rows past last: last's page)
+        const int j = (min(s0 + k, last) >> p.page_shift) - pg0;
+        return ((bad_pages >> j) & 1) != 0;
+    };
+    if (kPaged && bad_pages) {
+#pragma unroll
+        for (int b = 0; b < NST; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (bad_key(32 * b + acc_row(r, lane))) s[b][r] = -INFINITY;
     }
 
     // ---- Softmax against the exact row max; fp16 P^T fragments. ----
@@ -2231,6 +2288,14 @@ void kf_attn_decode_short_kernel(AttnParams p) {
     // d = 32 td + 16 (G % 2) + 4 (w % 4).  D = 16: groups with d >= 16 give
     // the zero rows 16..31 of V^T (their reads, of valid rows, are discarded).
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the slot's LDS-DMA has landed
+    if (kPaged && bad_pages) {
+        // V rows of invalid pages (loaded from page 0) -> zeros, so that their
+        // P = 0 meets finite values.
+        wave_lds_sync();
+        for (int i = lane; i < kKeys * kChunks; i += 64)
+            if (bad_key(i / kChunks)) *reinterpret_cast<u32x4*>(vs + i * 16) = u32x4{0u, 0u, 0u, 0u};
+        wave_lds_sync();
+    }
     const int G = lane >> 4, w = lane & 15;
     f32x16 o[kNTD];
 #pragma unroll
@@ -2279,6 +2344,20 @@ void kf_attn_decode_short_kernel(AttnParams p) {
             if (g == 0) store_stats(p, ri, m_nat, empty ? 0.f : l);
         }
     }
+}
+
+template <int D, int NST>
+__global__ __launch_bounds__(64 * kShortWaves, D >= 256 ? 1 : 2)
+void kf_attn_decode_short_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(1024))) char vbuf[kShortWaves * ShortCfg<D, NST>::kVBytes];
+    decode_short_body<D, NST, false>(p, vbuf);
+}
+
+template <int D, int NST>
+__global__ __launch_bounds__(64 * kShortWaves, D >= 256 ? 1 : 2)
+void kf_attn_decode_short_paged_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(1024))) char vbuf[kShortWaves * ShortCfg<D, NST>::kVBytes];
+    decode_short_body<D, NST, true>(p, vbuf);
 }
 
 // ---------------------------------------------------------------------------

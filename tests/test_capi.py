@@ -537,12 +537,12 @@ def test_paged_decode_validation():
     assert _paged(flags=16) == kf.KF_ERR_FLAGS
     assert _paged(flags=kf.KF_ATTN_OUT_F16 | kf.KF_ATTN_OUT_BF16) == kf.KF_ERR_FLAGS
     need = kf.paged_workspace_bytes(2, 1, 32, 8, 128, 16, 64)
-    # Paged decode always runs the streaming kernel: 4 splits of 256 keys (one
-    # 32-key stage per wave of an 8-wave workgroup) over the 1024-key
-    # capacity, each a partial of 2 x 32 rows of D + 2 floats (the same shape
-    # unpaged runs 32-key one-wave splits).
-    assert need == 4 * 64 * (128 + 2) * 4
-    assert kf.workspace_bytes(2, 1, 64 * 16, 32, 8, 128) == 32 * 64 * (128 + 2) * 4
+    # Paged decode is planned as the contiguous decode over the capacity
+    # (64 pages x 16 rows = 1024 keys): here the short-split kernel's 32
+    # one-wave splits of 32 keys, each a partial of 2 x 32 rows of D + 2
+    # floats.
+    assert need == 32 * 64 * (128 + 2) * 4
+    assert kf.workspace_bytes(2, 1, 64 * 16, 32, 8, 128) == need
     assert _paged(ws_bytes=need - 1) == kf.KF_ERR_WORKSPACE
     assert kf.paged_workspace_bytes(2, 9, 32, 8, 128, 16, 64) == 0    # not a decode shape
     assert kf.paged_workspace_bytes(2, 1, 32, 8, 128, 24, 64) == 0    # bad page size

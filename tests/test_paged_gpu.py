@@ -10,8 +10,10 @@ empty rows exactly O = 0, Mi = -inf, Li = 0.
 Cases: page sizes 16 (two pages per 32-row stage) to 256, random page
 permutations (the reference's worst-case fragmentation), GQA / MQA / MHA,
 q_len 1 and small causal q_len, every head dimension, ragged and empty
-sequences, invalid page ids inside a sequence; and bitwise equality with the
-contiguous decode kernel when the pages hold the same rows in order.
+sequences, invalid page ids inside a sequence, on both decode kernels (the
+short-split kernel's paged form for small jobs, the streaming kernel for
+large ones); and bitwise equality with the contiguous decode of either
+kernel when the pages hold the same rows in order.
 """
 import numpy as np
 import pytest
@@ -92,7 +94,25 @@ PAGED_CASES = [
     (2, 8, 2, 4, 256, 32, 12, [350, 200], True, ()),          # D=256, causal q_len=4
     (2, 32, 8, 1, 128, 16, 64, [1024, 1000], False, [(0, 3, -5), (1, 10, 10 ** 6)]),
     (4, 32, 4, 1, 128, 128, 33, [4200, 3000, 129, 4224], False, ()),
+    # Jobs large enough for the streaming decode kernel (the ones above run
+    # the short-split kernel's paged form), with invalid page ids.
+    (12, 32, 8, 1, 128, 16, 256, [4096 - 53 * b for b in range(12)], False,
+     [(0, 3, -5), (5, 200, 10 ** 6)]),
+    (24, 16, 16, 1, 64, 64, 40, [2560 - 100 * b for b in range(24)], False, [(7, 0, -1)]),
+    (12, 32, 8, 2, 256, 32, 64, [2048 - 77 * b for b in range(12)], True, [(11, 9, -2)]),
 ]
+
+
+def test_paged_cases_reach_both_decode_kernels():
+    """The cases above run the short-split decode kernel's paged form and the
+    streaming kernel's (the planner sizes a paged decode like a contiguous one
+    over the capacity): both appear, both with invalid page ids."""
+    import kernelfoundry_amd as kf
+    kinds = set()
+    for B, H_q, H_kv, q_len, D, ps, max_pages, kv_lens, causal, bad in PAGED_CASES:
+        p = kf.plan(B, q_len, ps * max_pages, H_q, H_kv, D)
+        kinds.add((p.splits_per_block == kf.plan(1, 1, 4096, 32, 8, 128).splits_per_block, bool(bad)))
+    assert kinds >= {(True, True), (False, True), (True, False)}
 
 
 @pytest.mark.parametrize("case", PAGED_CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_q{}_D{}_ps{}_{}{}".format(
@@ -109,13 +129,42 @@ def test_paged_decode_parity(case):
     _check(got, ref, f"case {case}")
 
 
+@pytest.mark.parametrize("page_size", [16, 32, 64])
+def test_paged_short_split_in_order_equals_contiguous_bitwise(page_size):
+    """The configs[1] decode (B = 1, 32 / 8 heads, 4096 keys) over pages that
+    hold a contiguous cache's rows in order: the short-split kernel's paged
+    form computes exactly what its contiguous form computes (same splits,
+    same loads, same arithmetic), O, Mi and Li bit for bit, also with a key
+    count that ends inside a page."""
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    B, H_q, H_kv, D, max_pages = 1, 32, 8, 128, 4096 // page_size
+    cap = max_pages * page_size
+    assert kf.plan(B, 1, cap, H_q, H_kv, D).splits_per_block == 4   # short-split kernel
+    q16, k16, v16 = orc.normal_fp16_inputs(B, H_q, H_kv, 1, cap, D, 2718)
+    to_pages = lambda a: a.reshape(B, H_kv, max_pages, page_size, D).transpose(0, 2, 1, 3, 4) \
+        .reshape(B * max_pages, H_kv, page_size, D)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    # Pages in a shuffled pool, the table pointing at them in order.
+    perm = np.random.default_rng(page_size).permutation(B * max_pages).astype(np.int32)
+    kp, vp = np.empty_like(to_pages(k16)), np.empty_like(to_pages(v16))
+    kp[perm], vp[perm] = to_pages(k16), to_pages(v16)
+    table = perm.reshape(B, max_pages)
+    for klen in (cap, cap - 7):
+        _announce(test="paged_short_vs_contiguous", page_size=page_size, kv_len=klen)
+        lens = np.array([klen], dtype=np.int32)
+        Op, Mp, Lp = kf.attn_decode_paged(t(q16), t(kp), t(vp), t(table), t(lens), return_stats=True)
+        Oc, Mc, Lc = kf.attn_fwd(t(q16), t(k16), t(v16), kv_lens=t(lens), return_stats=True)
+        torch.cuda.synchronize()
+        assert torch.equal(Op, Oc) and torch.equal(Mp, Mc) and torch.equal(Lp, Lc)
+
+
 @pytest.mark.parametrize("page_size", [16, 64])
 def test_paged_in_order_equals_contiguous_bitwise(page_size):
     """Pages holding the rows of a contiguous cache in order: the paged kernel
     computes exactly what kf_attn_fwd_ex computes on the contiguous cache
     (same splits, same stages, same arithmetic).  The batch is large enough
-    for the contiguous plan to use the streaming decode kernel too (paged
-    decode always does)."""
+    for the streaming decode kernel on both."""
     import kernelfoundry_amd as kf
     torch = _torch()
     B, H_q, H_kv, D, max_pages = 12, 32, 8, 128, 4096 // page_size
