@@ -50,10 +50,14 @@ long long decode_stream_splits(long long n_groups, long long max_splits, int D, 
     return best;
 }
 // Short-split decode (one wave per split of 32 or 64 keys): used while the
-// job is at most kShortMaxWavesPerCU such waves per CU; beyond it the work is
-// bandwidth-bound and the streaming decode kernel takes over.  64-key splits
-// are preferred while they still give kShortMinWavesPerCU waves per CU.
-constexpr long long kShortMaxWavesPerCU = 8;
+// job is at most kShortMaxWavesPerCU such waves per CU; beyond it the
+// streaming decode kernel takes over.  64-key splits are preferred while they
+// still give kShortMinWavesPerCU waves per CU.  Measured (MI355X, rotated
+// inputs, one process): with 8 waves per CU allowed, the 2048-wave jobs (e.g.
+// 2 x 8192, 8 x 2048 or 16 x 1024 keys at 32 / 8 heads) ran 1.23-1.26x
+// slower than on the streaming kernel and 1536-wave jobs 1.04-1.13x; jobs of
+// <= 1024 waves (configs[1], 8 x 1024 keys) are faster on the short kernel.
+constexpr long long kShortMaxWavesPerCU = 4;
 constexpr long long kShortMinWavesPerCU = 4;
 constexpr int kMinGroupKeys = 128;      // keys before a prefill row's keys are split between KV groups
 // Keys each KV group of a prefill workgroup keeps in a KV partition (split

@@ -217,9 +217,9 @@ def test_decode_split_geometry_covers_kv(B, q, kv, H_q, H_kv, D):
     splits = B * H_kv * p.num_splits
     if p.splits_per_block == 4:
         # Short-split kernel: one wave per split of 32 or 64 keys (64 only for
-        # D <= 128), 4 per workgroup, at most 8 waves per CU.
+        # D <= 128), 4 per workgroup, at most 4 waves per CU.
         assert p.kv_per_split in ((32, 64) if D <= 128 else (32,))
-        assert p.grid_blocks == -(-splits // 4) and p.block_threads == 256 and splits <= 2048
+        assert p.grid_blocks == -(-splits // 4) and p.block_threads == 256 and splits <= 4 * 256
     else:
         # Streaming kernel: 8 waves (4 at D = 256), at least one 32-key stage
         # per wave in every split.
@@ -239,7 +239,8 @@ def test_decode_split_geometry_covers_kv(B, q, kv, H_q, H_kv, D):
 @pytest.mark.parametrize("B,H_kv,kv,D,splits,per_block", [
     (1, 8, 131072, 128, 32, 1), (1, 1, 262144, 128, 249, 1), (1, 1, 65536, 64, 228, 1),
     (1, 1, 1 << 20, 16, 251, 1), (1, 4, 40000, 256, 125, 1), (1, 8, 8192, 128, 128, 4),
-    (1, 8, 4096, 128, 128, 4), (1, 8, 16384, 128, 256, 4), (2, 8, 16384, 128, 16, 1),
+    (1, 8, 4096, 128, 128, 4), (1, 8, 16384, 128, 32, 1), (2, 8, 16384, 128, 16, 1),
+    (2, 8, 8192, 128, 16, 1), (8, 8, 1024, 128, 16, 4),
     (12, 8, 4096, 128, 8, 1), (32, 8, 8192, 128, 1, 1),
 ])
 def test_decode_split_counts(B, H_kv, kv, D, splits, per_block):
@@ -249,7 +250,7 @@ def test_decode_split_counts(B, H_kv, kv, D, splits, per_block):
     partials the split merge reads in one pass, the key counts then rounded
     to whole 32-key stages; D = 256 (4 waves) aims at two workgroups per CU.
     Short-split decode: 64-key splits while they give 4 waves per CU, else
-    32-key ones, up to 8 waves per CU and 256 splits."""
+    32-key ones, up to 4 waves per CU and 256 splits."""
     p = kf.plan(B, 1, kv, 32, H_kv, D)
     assert p.path == ("decode_split" if splits > 1 else "decode") and p.num_splits == splits
     assert p.splits_per_block == per_block
@@ -358,13 +359,15 @@ def test_plans_scale_with_the_device_cu_count(cus):
     # those take less time (80 CUs: 7 rounds of 256 rows against 4 of 512).
     wide_c3 = rounds(256) * 512 * 0.94 < rounds(512) * 256
     assert kf.plan(1, 4096, 4096, 32, 8, 128, num_cus=cus).grid_blocks == (256 if wide_c3 else 512)
-    # C2 decode: short splits while 1024 one-wave splits fit 8 per CU.
+    # C2 decode: short splits while the one-wave splits fit 4 per CU.
     p = kf.plan(1, 1, 4096, 32, 8, 128, num_cus=cus)
     w64, w32 = 8 * 64, 8 * 128                   # waves of 64- and 32-key splits
-    if 4 * cus <= w64 <= 8 * cus:                # 64-key splits give 4 to 8 waves per CU
+    if w64 == 4 * cus:                           # 64-key splits give exactly 4 waves per CU
         assert p.splits_per_block == 4 and p.kv_per_split == 64
-    elif w32 <= 8 * cus:
+    elif w32 <= 4 * cus:
         assert p.splits_per_block == 4 and p.kv_per_split == 32
+    elif w64 <= 4 * cus:
+        assert p.splits_per_block == 4 and p.kv_per_split == 64
     else:
         assert p.splits_per_block == 1
     if cus == 32:

@@ -49,7 +49,7 @@ def _cases(n=40, seed=2026):
         out.append((B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens, int(rng.integers(1 << 30))))
     # Layouts random small shapes rarely reach: decode without split (at most
     # 32 keys), 8-wave workgroups (a grid of >= 256 workgroups x 256 rows),
-    # the streaming decode kernel (more than 2048 short splits) with and
+    # the streaming decode kernel (more than 1024 short splits) with and
     # without the merge, 64-key short splits and a merge over 256 splits.
     out.append((3, 8, 8, 1, 30, 128, True, [30, 0, 17], 11))
     out.append((2, 64, 8, 1024, 200, 64, True, [200, 150], 12))
