@@ -36,6 +36,10 @@ half of the metric):
                      B=8 KV=512/1024, MQA KV=512/1024; tests/bench_flash_attn.cu:
                      154-159, 181-182), each rotated over > 512 MB of sets,
                      with the same read floor and an oracle spot check.
+  * ``decode_kv4096_by_batch`` -- configs[1]'s decode at B = 2 .. 32 (rotated,
+                     spot-checked): where the KV=4096 decode turns from
+                     latency-bound to HBM-bound; ``decode.kv4096_by_batch``
+                     repeats it compactly as [B, us, fraction of peak].
   * ``sweep``     -- prefill S = 512 / 1024 / 2048 (configs[0] / [2] sweep),
                      the MQA D=64 configs[3] and the configs[2] shape at
                      D=256 (the reference's largest head dimension), plain
@@ -744,6 +748,24 @@ def main():
         del r
         torch.cuda.empty_cache()
 
+    # configs[1]'s KV=4096 decode at larger batches (the north star's "KV=4096
+    # decode" names no batch): B=1 is latency-bound, from a few sequences on
+    # the step streams HBM.  Rotated like the rows above.
+    print("bench: decode KV=4096 by batch", file=sys.stderr, flush=True)
+    kv4096_batch = []
+    for B in (2, 4, 8, 16, 32):
+        by = nbytes(B, 32, 8, 1, 4096, 128)
+        n_sets = int(min(4000, math.ceil(ROTATE_BYTES / by)))
+        d, r = run_decode(B, 4096, n_sets)
+        kv4096_batch.append({
+            "B": B, "kv_len": 4096, "H_q": 32, "H_kv": 8, "D": 128, "sets_rotated": n_sets,
+            "latency_us": round(d["latency_us"], 3), "hbm_gbs": round(d["gbs"], 1),
+            "frac": round(d["gbs"] / PEAK_HBM_GBS, 4), "bytes": by, "passes": PASSES,
+            "kernels": kf.kernel_names(B, 1, 4096, 32, 8, 128),
+            "parity": parity_spot_check(torch, r, [(0, 0), (B - 1, 31)])})
+        del r
+        torch.cuda.empty_cache()
+
     print("bench: sweep", file=sys.stderr, flush=True)
     sweep = [run_prefill(S) for S in (512, 1024, 2048)]
     sweep.append(run_prefill(2048, H_kv=1, D=64))
@@ -884,6 +906,7 @@ def main():
         "decode_paged": results["decode_paged"],
         "decode_paged_c1": results["decode_paged_c1"],
         "decode_sweep": decode_sweep,
+        "decode_kv4096_by_batch": kv4096_batch,
         "sweep": sweep,
         "parity": pre.get("parity"),
     }
@@ -909,6 +932,9 @@ def main():
         "sets_rotated": dec["sets_rotated"], "passes": PASSES,
         "kernels": kf.kernel_names(1, 1, 4096, 32, 8, 128),
         "parity_max_abs": dec["parity"]["max_abs"], "parity_rel_l2": dec["parity"]["rel_l2"],
+        # [B, us per step, fraction of HBM peak] of the same decode at larger batches
+        "kv4096_by_batch": [[1, round(dec["latency_us"], 2), round(dec["gbs"] / PEAK_HBM_GBS, 3)]] + [
+            [b["B"], round(b["latency_us"], 2), round(b["frac"], 3)] for b in kv4096_batch],
     }
     print(json.dumps(line), flush=True)
 
