@@ -46,7 +46,9 @@ half of the metric):
                      and causal (visible-pair FLOPs), S = 512 / 1024 at
                      D=256 (small grids: two KV groups per workgroup), and
                      configs[2] with a per-sequence key count of 4000 (FLOPs
-                     over those keys), and chunked prefill (q_len = 16 / 64 /
+                     over those keys), causal prefill at 2 x 4096 and 1 x 8192
+                     queries (grids that take the wide layout's causal kernel;
+                     visible-pair FLOPs, spot-checked), and chunked prefill (q_len = 16 / 64 /
                      128 / 256 query rows against 4096-16384 keys, 32 / 8 heads,
                      D = 128, and 64 x 4096 at D = 256:
                      the split prefill's KV partitions + split merge, the
@@ -613,15 +615,15 @@ def main():
     results = {}
 
     def run_prefill(S, H_kv=8, D=128, steps_=steps, check=None, causal=False, key_count=None,
-                    passes=PASSES):
-        sets = [_inputs(torch, 1, 32, H_kv, S, S, D, 1234 + S)]
+                    passes=PASSES, B=1):
+        sets = [_inputs(torch, B, 32, H_kv, S, S, D, 1234 + S)]
         lens = None if key_count is None else torch.full((1,), key_count, dtype=torch.int32, device="cuda")
         r = Runner(torch, kf, sets, D, flags=kf.KF_ATTN_CAUSAL if causal else 0, kv_lens=lens)
         ms, kern_mean, kern_med = time_steps(torch, r, steps_, warmup, passes)
         if causal:
-            f = causal_flops(1, 32, S, D)
+            f = causal_flops(B, 32, S, D)
         else:
-            f = flops(1, 32, S, S if key_count is None else key_count, D)
+            f = flops(B, 32, S, S if key_count is None else key_count, D)
         out = {"S": S, "H_kv": H_kv, "D": D, "ms": ms, "tflops": f / (ms * 1e9),
                "frac": round(f / (ms * 1e9) / PEAK_FP16_TFLOPS, 4),
                "kernel_ms_mean": kern_mean, "kernel_tflops": f / (kern_mean * 1e9),
@@ -630,9 +632,11 @@ def main():
             out["causal"] = True
         if key_count is not None:
             out["key_count"] = key_count
-        out["kernels"] = kf.kernel_names(1, S, S, 32, H_kv, D, causal=causal, masked=key_count is not None)
+        if B > 1:
+            out["B"] = B
+        out["kernels"] = kf.kernel_names(B, S, S, 32, H_kv, D, causal=causal, masked=key_count is not None)
         if check:
-            out["parity"] = parity_spot_check(torch, r, check)
+            out["parity"] = parity_spot_check(torch, r, check, causal=causal)
         return out
 
     if args.only in (None, "prefill"):
@@ -775,6 +779,10 @@ def main():
     # configs[2] with a per-sequence key count (kf_attn_fwd_ex kv_lens): the
     # sequence uses its first 4000 of the 4096 allocated key rows.
     sweep.append(run_prefill(4096, key_count=4000))
+    # Causal prefill with two wide workgroups per CU or more (the wide
+    # layout's causal kernel): 2 x 4096 and 1 x 8192 queries, 32 / 8 heads.
+    sweep.append(run_prefill(4096, causal=True, B=2, check=[(0, 0), (1, 31)]))
+    sweep.append(run_prefill(8192, causal=True, check=[(0, 31)]))
     # Chunked prefill (a short chunk of query rows against a long cache): the
     # split prefill's KV partitions + split merge.
     for q, kv, D in ((16, 8192, 128), (64, 4096, 128), (128, 8192, 128), (256, 16384, 128),

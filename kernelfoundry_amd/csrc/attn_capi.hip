@@ -84,6 +84,12 @@ constexpr double kWide256RowCost = 0.7;
 // 25.5 vs 30.7 at S = 512, 32 / 8.  Where the 256-row kernel is taken it
 // stays ahead (S = 1536-5120, 32 / 8 heads: the KV groups 1-6 % slower).
 constexpr int kWide256GroupKeys = 2 * kMinGroupKeys;
+// Causal calls at D = 64 / 128 take the wide kernel from this many keys per
+// query row on average (kv_len - q_len / 2, two wide workgroups per CU or
+// more): against the 256-row kernel, A/B in one process, 2 x 4096 and 1 x 8192
+// queries at 32 / 8 heads 1.08-1.09x (D = 64 1.02-1.06x), 2 x 4096 queries
+// against 6144 keys 1.09x, but 4 x 2048 queries 0.88x.
+constexpr int kWideCausalMinKeys = 2048;
 constexpr size_t kWsAlign = 256;
 
 thread_local int g_last_hip_error = 0;
@@ -139,6 +145,7 @@ struct Plan {
                         // 0 = the 32-row-per-wave kernel
     int wide_grid;      // workgroups of the wide kernel
     int wide_kv_groups; // KV groups of the wide kernel (2: D = 256, 128 rows per workgroup)
+    bool wide_causal;   // D = 64 / 128: causal calls take the wide kernel too
     int short_stages;   // decode: 32-key stages per split of the short-split kernel, 0 = streaming kernel
     int merge_cw;       // split merge: float4 columns per wave
     int merge_per;      // split merge: splits per lane
@@ -262,8 +269,8 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
         // kernel (64 rows per wave, 512 per workgroup) when its rounds of
         // workgroups take less time than the 256-row kernel's; one workgroup
         // runs per CU in either kernel, and a wide row costs kWideRowCost of
-        // a 256-row-kernel row (also for calls with key counts; causal ones
-        // keep the 256-row kernel).  D = 256, masked calls included: the
+        // a 256-row-kernel row (also for calls with key counts, and causal
+        // ones when wide_causal, below).  D = 256, masked calls included: the
         // wide kernels' 8 waves x 32 rows against 4 waves x 32 rows, by the
         // same rule (kWide256RowCost), else, from kWide256GroupKeys keys on,
         // the wide kernel with two KV groups on the 4-wave kernel's tiles.
@@ -278,6 +285,18 @@ int make_plan(int B, int q_len, int kv_len, int H_q, int H_kv, int D, const Devi
                 p.wide_row_tiles = (int)wrt;
                 p.wide_grid = (int)wg;
                 p.wide_kv_groups = 1;
+                // Causal row tiles differ in length up to the whole key range:
+                // dealt longest first, they fill every CU evenly once there
+                // are two workgroups per CU or more (the average load per CU
+                // then exceeds the longest tile); with fewer, the longest
+                // tiles set the launch and the 256-row kernel's twice as many
+                // tiles balance better.  A wave's 64 rows must lie in one
+                // head (q_len a multiple of 64), and the rows must see
+                // kWideCausalMinKeys keys on average: the waves of a 512-row
+                // tile end up to 14 tiles apart, and a SIMD whose partner has
+                // finished runs its last tiles alone.
+                const long long avg_keys = (long long)kv_len - q_len / 2;
+                p.wide_causal = wg >= 2LL * cus && q_len % 64 == 0 && avg_keys >= kWideCausalMinKeys;
             } else if (D == 256 && kv_len >= kWide256GroupKeys) {
                 p.wide_row_tiles = p.row_tiles;  // 128 rows per workgroup
                 p.wide_grid = p.grid;
@@ -405,12 +424,15 @@ hipError_t launch_prefill_kernel(const Plan& pl, const kf::AttnParams& prm, hipS
             }
         }
         if constexpr (D == 64 || D == 128) {
-            // Two row blocks per wave: key counts give both one limit, so
-            // only causal calls stay on the 256-row kernel.
-            if (!prm.causal && pl.wide_row_tiles > 0) {
+            // Causal calls take the wide layout's causal kernel when its grid
+            // balances (wide_causal), else the 256-row kernel.
+            if (pl.wide_row_tiles > 0 && (!prm.causal || pl.wide_causal)) {
                 kf::AttnParams pw = prm;
                 pw.row_tiles = pl.wide_row_tiles;
-                if (mask)
+                if (prm.causal)
+                    kf::kf_attn_prefill_wide_kernel<D, true, 1, true><<<dim3(pl.wide_grid),
+                                                                dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
+                else if (mask)
                     kf::kf_attn_prefill_wide_kernel<D, true, 1><<<dim3(pl.wide_grid),
                                                                   dim3(kf::WideCfg<D>::kThreads), 0, stream>>>(pw);
                 else
@@ -694,9 +716,11 @@ int kf_attn_kernel_names(int B, int q_len, int kv_len, int H_q, int H_kv, int D,
     if (prefill_path(pl.path)) {
         const bool causal = (flags & KF_ATTN_CAUSAL) != 0;
         const bool mask = causal || kv_lens;
-        if (pl.wide_row_tiles > 0 && (!causal || D >= 256))
-            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d, %s, %d>", D, mask ? "true" : "false",
-                         pl.wide_kv_groups);
+        if (pl.wide_row_tiles > 0 && causal && D < 256 && pl.wide_causal)
+            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d, true, 1, true>", D);
+        else if (pl.wide_row_tiles > 0 && (!causal || D >= 256))
+            n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_wide_kernel<%d, %s, %d, false>", D,
+                         mask ? "true" : "false", pl.wide_kv_groups);
         else if (D >= 256 && pl.path == KF_PATH_PREFILL_SPLIT)
             n = snprintf(tmp, sizeof(tmp), "kf_attn_prefill_parts_kernel<%d, %s>", D, mask ? "true" : "false");
         else

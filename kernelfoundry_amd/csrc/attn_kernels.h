@@ -1401,15 +1401,23 @@ template <int D> struct WideCfg {
 };
 
 // kMask: causal masking and/or per-sequence key counts, as in
-// kf_attn_prefill_kernel.  Causal masking needs one row block per wave
-// (D = 256); with two (D = 64 / 128) the host launches the masked kernel
-// for key counts only, which give every row of a sequence the same limit.
+// kf_attn_prefill_kernel.  With one row block per wave (D = 256) causal
+// masking is part of the masked kernel.  With two (D = 64 / 128) the masked
+// kernel serves key counts, which give every row of a sequence one limit, and
+// causal calls run kCausal2: each wave on 64 consecutive rows (block 1 =
+// block 0 + 32 rows instead of the same rows in the second half of the
+// workgroup), so that its blocks' key limits differ by one tile, each block
+// masked against its own limits; a row of kCausal2 keeps its block limit
+// unclamped (one register), which needs a wave's 64 rows inside one head.  At
+// D = 128 kCausal2 derives its K and V^T read offsets by XOR: the registers
+// that frees keep its tile loop from spilling.  kCausal2 = false leaves the
+// other instantiations instruction for instruction as they compile without it.
 // KS > 1 (D = 256): KV groups as in kf_attn_prefill_kernel — the waves form
 // KS groups of NW / KS, each on the same rows and its own share of the keys,
 // merged through LDS at the end; for grids too small for 256-row tiles.
 // (The body sits in the kernel itself: moved into a shared device function,
 // the unmasked kernel compiled to a different, 0.5 % slower schedule.)
-template <int D, bool kMask, int KS>
+template <int D, bool kMask, int KS, bool kCausal2 = false>
 __global__ __launch_bounds__(WideCfg<D>::kThreads, 2)
 void kf_attn_prefill_wide_kernel(AttnParams p) {
     static_assert(D == 64 || D == 128 || D == 256, "wide prefill: D = 64, 128 or 256");
@@ -1420,8 +1428,9 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     constexpr bool kQ1Lds = Cfg::kQ1Lds;
     constexpr bool kPipe = Cfg::kPipe;
     constexpr int kRB = Cfg::kRB;
-    constexpr bool kXorOff = Cfg::kXorOff;
+    constexpr bool kXorOff = Cfg::kXorOff || (kCausal2 && D == 128);
     static_assert(KS == 1 || (KS == 2 && kRB == 1 && !kPipe && SR == BC), "KV groups: D = 256, two groups");
+    static_assert(!kCausal2 || (kMask && kRB == 2 && KS == 1), "causal two-block layout");
     constexpr int kRowWaves = NW / KS;                 // waves per KV group
     constexpr int kRows = 32 * kRB * kRowWaves;        // query rows per workgroup
     using S = DmaStage<D, SR, kRowWaves>;
@@ -1446,8 +1455,13 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     // Row wave.  Causal: waves w and w + 4 share a SIMD and get row blocks w
     // and 7 - w, so that the fully masked tiles each wave skips add up to the
     // same count on every SIMD.
-    // Causal masking is compiled in for one row block per wave only.
-    const bool causal = kMask && kRB == 1 && p.causal;
+    // Causal masking: one row block per wave, or the two-block layout of
+    // kCausal2 (compiled out of the other two-block kernels).
+    const bool causal = kMask && (kRB == 1 || kCausal2) && p.causal;
+    // Rows of one wave: 32 (one block), or 64 consecutive ones when causal
+    // with two blocks; b1_off: the offset of block 1 from block 0.
+    const int wave_rows = (kRB == 2 && causal) ? 64 : 32;
+    const int b1_off = (kRB == 2 && causal) ? 32 : kRows / 2;
     const int wave = KS == 1 ? ((causal && wave_id >= 4) ? 11 - wave_id : wave_id) : wave_id % kRowWaves;
     const int kgrp = KS == 1 ? 0 : wave_id / kRowWaves;  // KV group
     const int g = lane >> 5;
@@ -1480,9 +1494,9 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             int lo, hi;
             qi_range(r0, r1, q_len, lo, hi);
             blk_lim = row_kv_limit(p, kvb, hi);
-            const int w0 = r0 + wave * 32;
+            const int w0 = r0 + wave * wave_rows;
             if (w0 < R) {
-                qi_range(w0, min(R, w0 + 32) - 1, q_len, lo, hi);
+                qi_range(w0, min(R, w0 + wave_rows) - 1, q_len, lo, hi);
                 wave_min = row_kv_limit(p, kvb, lo);
                 wave_max = row_kv_limit(p, kvb, hi);
             } else {
@@ -1594,11 +1608,12 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     static_assert(!kXorOff || D >= 128, "XOR offsets use the D >= 128 swizzle");
     const int kbase = koff[0], vbase = voff[0][0];
 
-    // Row blocks: block 0 = rows [rt kRows + 32 w, + 32), block 1 = the same
-    // in the second half of the workgroup's rows.  Rows past R compute on
-    // row R - 1 and are never stored.
-    const int row0 = rt * kRows + wave * 32 + (lane & 31);
-    const int row1 = row0 + kHalfRows;
+    // Row blocks: block 0 = rows [rt kRows + wave_rows w, + 32), block 1 =
+    // block 0 + b1_off (the same rows in the second half of the workgroup's
+    // rows, or, causal, the next 32).  Rows past R compute on row R - 1 and
+    // are never stored.
+    const int row0 = rt * kRows + wave * wave_rows + (lane & 31);
+    const int row1 = row0 + b1_off;
     if (kMask && ntiles == 0) {
         // No key for any row of this workgroup (workgroup-uniform).
 #pragma unroll
@@ -1617,8 +1632,16 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
         return;
     }
     // This lane's query row sees keys [0, lim_lane) (padding rows: blk_lim).
+    // Causal with two blocks (the host keeps a wave's 64 rows inside one
+    // head): lim_lane holds block 0's limit before clamping to [0, kvb], and
+    // block 1's row, 32 queries on, sees keys [0, clamp(lim_lane + 32)).
     int lim_lane = kv_len;
-    if constexpr (kMask) lim_lane = !causal ? kvb : row0 < R ? row_kv_limit(p, kvb, row0 % p.q_len) : blk_lim;
+    if constexpr (kMask) {
+        if (kCausal2 && causal)
+            lim_lane = row0 < R ? row0 % p.q_len + kvb - p.q_len + 1 : blk_lim;
+        else
+            lim_lane = !causal ? kvb : row0 < R ? row_kv_limit(p, kvb, row0 % p.q_len) : blk_lim;
+    }
     if constexpr (KS > 1) lim_lane = min(lim_lane, kv_end) - kv_base;
 
     issue_stage(b0, 0);
@@ -1633,9 +1656,11 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
         const int lr = lane / S::kChunks;
 #pragma unroll
         for (int j0 = 0; j0 < kQInstr; j0 += NW) {
-            const int j = j0 + wave;
+            const int j = j0 + wave_id;
             const int r = j * S::kRowsPerInstr + lr;
-            const int src = min(rt * kRows + kHalfRows + r, R - 1);
+            // LDS row r holds block-1 row r % 32 of wave r / 32.
+            const int src = min(rt * kRows + (kCausal2 ? (r >> 5) * wave_rows + b1_off + (r & 31)
+                                                        : kHalfRows + r), R - 1);
             const uint32_t off = (uint32_t)src * S::kRowBytes +
                                  (uint32_t)((((lane % S::kChunks) ^ SW::h(r)) % S::kChunks) * 16);
             __builtin_amdgcn_global_load_lds(Qb + off, (lds_void*)(q1_lds + j * 1024), 16, 0, 0);
@@ -1685,12 +1710,25 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
         if ((t + 1) * BC > wave_min) {
             asm volatile("" ::: "memory");
             const int lg = lim_lane - t * BC - 4 * g;
+            if constexpr (kCausal2) {
+                // One block at a time: a second limit live across the tile
+                // would cost a register that this kernel does not have.
+                int lb = (causal ? min(max(lim_lane, 0), kvb) : lim_lane) - t * BC - 4 * g;
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (8 * (r >> 2) + (r & 3) >= lg) {
-                    s0[0][r] = -INFINITY;
-                    if constexpr (kRB == 2) s1[0][r] = -INFINITY;
-                }
+                for (int r = 0; r < 16; ++r)
+                    if (8 * (r >> 2) + (r & 3) >= lb) s0[0][r] = -INFINITY;
+                lb = (causal ? min(max(lim_lane + 32, 0), kvb) : lim_lane) - t * BC - 4 * g;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (8 * (r >> 2) + (r & 3) >= lb) s1[0][r] = -INFINITY;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (8 * (r >> 2) + (r & 3) >= lg) {
+                        s0[0][r] = -INFINITY;
+                        if constexpr (kRB == 2) s1[0][r] = -INFINITY;
+                    }
+            }
         }
     };
     // O^T += V^T P^T for both row blocks, V rows at stage + kTensorBytes.
@@ -1729,7 +1767,7 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
                       st0.l);
             if constexpr (kRB == 2) {
                 block_update_max<kNTD>(st1, block_rowmax<1>(s1), c, inv_c, o1);
-                block_exp(s1[0], c, -st1.m, p1[0], p1[1], st1.l);
+                block_exp(s1[0], c, (kCausal2 && st1.m == -INFINITY) ? 0.f : -st1.m, p1[0], p1[1], st1.l);
             }
             pv2(stage, p0, p1);
         };
@@ -1776,8 +1814,9 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
             f32x16 sn0[1], sn1[1];
             qk2(nxt, sn0, sn1);  // the last tile's reads a stale buffer, discarded
             f16x8 p0[2], p1[2];
-            block_exp(sc0[0], c, -st0.m, p0[0], p0[1], st0.l);
-            block_exp(sc1[0], c, -st1.m, p1[0], p1[1], st1.l);
+            // Causal: a row with no key yet keeps m = -inf and gets P = 0.
+            block_exp(sc0[0], c, (kCausal2 && st0.m == -INFINITY) ? 0.f : -st0.m, p0[0], p0[1], st0.l);
+            block_exp(sc1[0], c, (kCausal2 && st1.m == -INFINITY) ? 0.f : -st1.m, p1[0], p1[1], st1.l);
             pv2(cur, p0, p1);
             if (t + 1 < ntiles) {
                 tail_mask(sn0, sn1, t + 1);
@@ -1814,7 +1853,8 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
         return;
     }
 
-    // ---- Epilogue: both row blocks (unmasked, every row saw key 0, so l > 0). ----
+    // ---- Epilogue: both row blocks (masked rows without a visible key:
+    // O = 0, Mi = -inf, Li = 0). ----
     const float l0 = sum_xor32(st0.l);
     if (row0 < R) {
         const size_t ri = (size_t)grp * R + row0;
@@ -1827,10 +1867,14 @@ void kf_attn_prefill_wide_kernel(AttnParams p) {
     if (kRB == 2 && row1 < R) {
         const float l1 = sum_xor32(st1.l);
         const size_t ri = (size_t)grp * R + row1;
-        store_o_row_any<D>(p, ri, o1, 1.0f / l1, g);
-        if (g == 0) store_stats(p, ri, st1.rmax * p.scale, l1 * rebase_factor(st1.m, st1.rmax, p.scale_log2));
+        const bool empty = kCausal2 && !(l1 > 0.f);  // causal: no visible key
+        store_o_row_any<D>(p, ri, o1, empty ? 0.f : 1.0f / l1, g);
+        if (g == 0)
+            store_stats(p, ri, st1.rmax * p.scale,
+                        empty ? 0.f : l1 * rebase_factor(st1.m, st1.rmax, p.scale_log2));
     }
 }
+
 
 // ---------------------------------------------------------------------------
 // Decode (split-KV): <= 32 query rows per KV head.  Workgroup = NW waves on

@@ -48,7 +48,7 @@ def test_roofline_point(line):
     r = line["roofline"]
     assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and r["peak"] == 2516.6
     assert r["frac"] == pytest.approx(r["achieved"] / r["peak"], abs=1e-3)
-    assert r["kernel"].startswith("kf_attn_prefill_wide_kernel<128, false, 1>")
+    assert r["kernel"].startswith("kf_attn_prefill_wide_kernel<128, false, 1, false>")
 
 
 def test_parity_spot_checks_pass(line):

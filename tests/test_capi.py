@@ -178,7 +178,7 @@ def test_plans_for_baseline_configs():
     assert p.path == "prefill" and p.rows_per_group == 4 * 4096
     assert p.block_threads == 512                    # 8 waves x 64 query rows
     assert p.grid_blocks == 8 * (4 * 4096 // 512) == 256
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false, 1, false>"
     # masked: the 256-row kernel (8 waves x 32 rows), 512 workgroups
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == "kf_attn_prefill_kernel<128, true, 8, 1>"
     p = kf.plan(1, 2048, 2048, 32, 8, 128)           # S = 2048: 128 wide workgroups would idle CUs
@@ -288,7 +288,7 @@ def test_prefill_waves_per_workgroup(S, H_kv, D, waves, groups):
         ks = 1 if -(-n256 // 256) * 256 * 0.7 < -(-n128 // 256) * 128 else 2 if S >= 256 else 0
         assert wide == (ks > 0)
     if wide and D == 256:
-        assert masked_name == f"kf_attn_prefill_wide_kernel<256, true, {ks}>"
+        assert masked_name == f"kf_attn_prefill_wide_kernel<256, true, {ks}, false>"
     else:
         assert masked_name.split(" + ")[0] == f"kf_attn_prefill_kernel<{D}, true, {waves}, {groups}>"
     if wide:
@@ -398,28 +398,52 @@ def test_plan_for_cus_rejects_bad_counts(lib):
     assert lib.kf_attn_plan_for_cus(1, 1, 1, 1, 1, 128, 80, None) == kf.KF_ERR_NULL
 
 
+def _assert_causal_wide_rule():
+    """Causal calls at D = 64 / 128 take the wide layout's causal kernel when
+    the wide grid has two workgroups per CU or more (256 CUs here: no device),
+    q_len is a multiple of 64 and the rows see kv_len - q_len / 2 >= 2048
+    keys on average; else the 256-row kernel."""
+    wide = "kf_attn_prefill_wide_kernel<{}, true, 1, true>"
+    narrow = "kf_attn_prefill_kernel<{}, true, 8, 1>"
+    for (B, q, kv, H_q, H_kv, D), want in [
+            ((2, 4096, 4096, 32, 8, 128), wide),      # 512 wide workgroups, 2048 keys per row
+            ((1, 8192, 8192, 32, 8, 128), wide),
+            ((2, 4096, 4096, 32, 8, 64), wide),
+            ((2, 4096, 6144, 32, 8, 128), wide),
+            ((1, 4096, 4096, 32, 8, 128), narrow),    # one wide workgroup per CU
+            ((4, 2048, 2048, 32, 8, 128), narrow),    # 1024 keys per row on average
+            ((2, 4096, 3000, 32, 8, 128), narrow),    # 952
+            ((2, 4032, 4096, 32, 8, 128), wide),      # q_len = 63 x 64: row tiles across heads
+            ((2, 4064, 4096, 32, 8, 128), narrow)]:   # q_len % 64 = 32
+        assert kf.kernel_names(B, q, kv, H_q, H_kv, D, causal=True) == want.format(D), (B, q, kv, D)
+        # unmasked and key-count calls of these shapes never take the causal kernel
+        assert not kf.kernel_names(B, q, kv, H_q, H_kv, D).endswith("true>")
+        assert not kf.kernel_names(B, q, kv, H_q, H_kv, D, masked=True).endswith(", true>")
+
+
 def test_kernel_names_follow_the_plan(lib):
     """kf_attn_kernel_names names the kernels in launch order, as the
     profiler lists them."""
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false, 1>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, masked=True) == "kf_attn_prefill_wide_kernel<128, true, 1>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128) == "kf_attn_prefill_wide_kernel<128, false, 1, false>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, masked=True) == "kf_attn_prefill_wide_kernel<128, true, 1, false>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 2048, 2048, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 1>"
     assert kf.kernel_names(1, 4096, 4096, 32, 8, 128, causal=True) == \
         "kf_attn_prefill_kernel<128, true, 8, 1>"
     assert kf.kernel_names(1, 512, 512, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 8, 4>"
     assert kf.kernel_names(1, 256, 256, 32, 8, 128) == "kf_attn_prefill_kernel<128, false, 4, 2>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_wide_kernel<256, false, 1>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, causal=True) == "kf_attn_prefill_wide_kernel<256, true, 1>"
-    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, masked=True) == "kf_attn_prefill_wide_kernel<256, true, 1>"
-    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256) == "kf_attn_prefill_wide_kernel<256, false, 2>"
-    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256, causal=True) == "kf_attn_prefill_wide_kernel<256, true, 2>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256) == "kf_attn_prefill_wide_kernel<256, false, 1, false>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, causal=True) == "kf_attn_prefill_wide_kernel<256, true, 1, false>"
+    assert kf.kernel_names(1, 4096, 4096, 32, 8, 256, masked=True) == "kf_attn_prefill_wide_kernel<256, true, 1, false>"
+    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256) == "kf_attn_prefill_wide_kernel<256, false, 2, false>"
+    assert kf.kernel_names(1, 2048, 2048, 16, 4, 256, causal=True) == "kf_attn_prefill_wide_kernel<256, true, 2, false>"
     assert kf.kernel_names(1, 2048, 255, 16, 4, 256) == "kf_attn_prefill_kernel<256, false, 4, 1>"
     assert kf.kernel_names(1, 2048, 255, 16, 4, 256, causal=True) == "kf_attn_prefill_kernel<256, true, 4, 1>"
     assert kf.kernel_names(1, 1, 4096, 32, 8, 128) == \
         "kf_attn_decode_short_kernel<128, 1> + kf_attn_split_merge_kernel<128, 8, 4>"
     assert kf.kernel_names(32, 1, 8192, 32, 8, 128) == "kf_attn_decode_kernel<128, false>"
     buf = ctypes.create_string_buffer(8)
+    _assert_causal_wide_rule()
     assert lib.kf_attn_kernel_names(1, 1, 4096, 32, 8, 128, 0, None, buf, 8) == kf.KF_ERR_SIZE
     assert lib.kf_attn_kernel_names(1, 1, 4096, 32, 8, 128, 0, None, None, 8) == kf.KF_ERR_NULL
     assert lib.kf_attn_kernel_names(1, 1, 4096, 32, 8, 100, 0, None, buf, 8) == kf.KF_ERR_HEAD_DIM

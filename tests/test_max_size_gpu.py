@@ -31,9 +31,9 @@ def test_last_key_at_the_offset_limit(q_len, H_q, D):
     split = q_len == 64
     masked = kf.kernel_names(1, q_len, kv, H_q, 1, D, masked=True)
     if wide:
-        assert names == f"kf_attn_prefill_wide_kernel<{D}, false, 1>", names
+        assert names == f"kf_attn_prefill_wide_kernel<{D}, false, 1, false>", names
         # ... and its masked instantiation, with the key count set to kv_len
-        assert masked == f"kf_attn_prefill_wide_kernel<{D}, true, 1>", masked
+        assert masked == f"kf_attn_prefill_wide_kernel<{D}, true, 1, false>", masked
     if split:
         assert kf.plan(1, q_len, kv, H_q, 1, D).path == "prefill_split"
         kern = "kf_attn_prefill_parts_kernel<256, " if D == 256 else f"kf_attn_prefill_kernel<{D}, "

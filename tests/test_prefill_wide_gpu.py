@@ -21,9 +21,12 @@ equal, bit for bit, that kernel's on the same inputs (PAIRS, below), and
 the masked wide kernel with every sequence's key count equal to kv_len must
 give the unmasked one's bits.
 
-Masked calls run kf_attn_prefill_wide_kernel<D, true, 1> when the planner
+Masked calls run kf_attn_prefill_wide_kernel<D, true, 1, false> when the planner
 chooses the wide grid: at D = 256 causal and/or per-sequence key counts, at
-D = 64 / 128 key counts only (causal calls keep the 256-row kernel).
+D = 64 / 128 key counts; causal calls at D = 64 / 128 run
+kf_attn_prefill_wide_kernel<D, true, 1, true> (each wave on 64 consecutive
+rows) when the wide grid has two workgroups per CU or more and the rows see
+2048 keys on average, else the 256-row kernel (CAUSAL_PAIRS, below).
 MASKED_CASES cover causal with q_len = kv_len, kv_len > q_len and q_len >
 kv_len (rows without keys), key counts with an empty sequence and a single
 key, both together, and GQA ratio 16, against the oracle with rows without
@@ -90,7 +93,7 @@ def test_wide_prefill_matches_oracle(case):
     B, H_q, H_kv, q_len, kv_len, D = case
     names = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D)
     print("case", case, names, flush=True)
-    assert names == f"kf_attn_prefill_wide_kernel<{D}, false, 1>", names
+    assert names == f"kf_attn_prefill_wide_kernel<{D}, false, 1, false>", names
     (q16, k16, v16), (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 11 + kv_len)
     O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True)
     torch.cuda.synchronize()
@@ -111,7 +114,7 @@ def test_wide_masked_without_masking_equals_unmasked_bitwise(case):
     B, H_q, H_kv, q_len, kv_len, D = case
     masked = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, masked=True)
     print("case", case, masked, flush=True)
-    assert masked == f"kf_attn_prefill_wide_kernel<{D}, true, 1>", masked
+    assert masked == f"kf_attn_prefill_wide_kernel<{D}, true, 1, false>", masked
     _, (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, D, 5)
     full = torch.full((B,), kv_len, dtype=torch.int32, device="cuda")
     Ow, Mw, Lw = kf.attn_fwd(Q, K, V, return_stats=True)
@@ -145,7 +148,7 @@ def test_wide_masked_prefill_matches_oracle(case):
     B, H_q, H_kv, q_len, kv_len, causal, kv_lens, D = case
     name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, D, causal=causal, masked=kv_lens is not None)
     print("case", case, name, flush=True)
-    assert name == f"kf_attn_prefill_wide_kernel<{D}, true, 1>", name
+    assert name == f"kf_attn_prefill_wide_kernel<{D}, true, 1, false>", name
     run_and_check(B, H_q, H_kv, q_len, kv_len, D, causal, kv_lens, 300 + q_len)
 
 
@@ -177,7 +180,7 @@ def test_wide_and_narrow_kernels_agree_bitwise(case):
     n2 = kf.kernel_names(2, S, kv, H_q, H_kv, D, causal=causal, masked=masked)
     print("case", case, n1, "|", n2, flush=True)
     assert n1.startswith("kf_attn_prefill_kernel<") and n2.startswith("kf_attn_prefill_wide_kernel<"), (n1, n2)
-    assert n2.endswith(", 1>"), n2  # one KV group: the 32-row kernel's operation order
+    assert n2.endswith(", 1, false>"), n2  # one KV group: the 32-row kernel's operation order
     _, (Q, K, V) = _inputs(2, H_q, H_kv, S, kv, D, 77)
     l1 = torch.tensor([k0], dtype=torch.int32, device="cuda") if masked else None
     l2 = torch.tensor([k0, kv - 5], dtype=torch.int32, device="cuda") if masked else None
@@ -216,7 +219,7 @@ def test_kv_group_wide_prefill_matches_oracle(case):
     mask = causal or kv_lens is not None
     name = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, 256, causal=causal, masked=kv_lens is not None)
     print("case", case, name, flush=True)
-    assert name == f"kf_attn_prefill_wide_kernel<256, {'true' if mask else 'false'}, 2>", name
+    assert name == f"kf_attn_prefill_wide_kernel<256, {'true' if mask else 'false'}, 2, false>", name
     run_and_check(B, H_q, H_kv, q_len, kv_len, 256, causal, kv_lens, 900 + kv_len)
 
 
@@ -227,7 +230,7 @@ def test_kv_group_masked_without_masking_equals_unmasked_bitwise(case):
     B, H_q, H_kv, q_len, kv_len = case[:5]
     masked = kf.kernel_names(B, q_len, kv_len, H_q, H_kv, 256, masked=True)
     print("case", case, masked, flush=True)
-    assert masked == "kf_attn_prefill_wide_kernel<256, true, 2>", masked
+    assert masked == "kf_attn_prefill_wide_kernel<256, true, 2, false>", masked
     _, (Q, K, V) = _inputs(B, H_q, H_kv, q_len, kv_len, 256, 6)
     full = torch.full((B,), kv_len, dtype=torch.int32, device="cuda")
     Ow, Mw, Lw = kf.attn_fwd(Q, K, V, return_stats=True)
@@ -235,3 +238,73 @@ def test_kv_group_masked_without_masking_equals_unmasked_bitwise(case):
     torch.cuda.synchronize()
     assert torch.equal(Ow, On), f"O differs: max {(Ow - On).abs().max().item():.3g}"
     assert torch.equal(Mw, Mn) and torch.equal(Lw, Ln), "Mi / Li differ"
+
+
+# Causal calls at D = 64 / 128: at q_len = 4096 (8192 at 16 / 8 heads) the
+# planner runs the 256-row kernel for B = 1 (one wide workgroup per CU) and
+# the wide layout's causal kernel for B = 2.  Each row sees the same tiles in
+# the same order in both (the wide kernel computes, for a wave's first 32
+# rows, tiles wholly masked for them, which add exactly nothing), so batch 0
+# of the B = 2 call must equal the B = 1 call bit for bit, O, Mi and Li,
+# also with key counts (rows without keys: O = 0, Mi = -inf, Li = 0) and with
+# row tiles that straddle heads (q_len = 5184 = 10.125 x 512).
+CAUSAL_PAIRS = [
+    # D, H_q, H_kv, q_len, kv_len, batch-0 key count (None: all keys)
+    (128, 32, 8, 4096, 4096, None),
+    (64, 32, 8, 4096, 4096, None),
+    (128, 32, 8, 4096, 6144, None),     # kv_len > q_len
+    (128, 32, 8, 4096, 4096, 1000),     # 3096 rows of batch 0 see no key
+    (64, 32, 8, 4096, 4608, 3333),
+    (128, 32, 8, 5184, 5184, None),     # row tiles across heads, padding rows
+    (128, 16, 8, 8192, 8192, None),     # GQA ratio 2
+]
+
+
+@pytest.mark.parametrize("case", CAUSAL_PAIRS, ids=lambda c: "D{}_Hq{}_Hkv{}_q{}_kv{}_{}".format(
+    *c[:5], "full" if c[5] is None else f"k{c[5]}"))
+def test_wide_causal_kernel_equals_256_row_kernel_bitwise(case):
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    D, H_q, H_kv, S, kv, k0 = case
+    masked = k0 is not None
+    n1 = kf.kernel_names(1, S, kv, H_q, H_kv, D, causal=True, masked=masked)
+    n2 = kf.kernel_names(2, S, kv, H_q, H_kv, D, causal=True, masked=masked)
+    print("case", case, n1, "|", n2, flush=True)
+    assert n1 == f"kf_attn_prefill_kernel<{D}, true, 8, 1>", n1
+    assert n2 == f"kf_attn_prefill_wide_kernel<{D}, true, 1, true>", n2
+    _, (Q, K, V) = _inputs(2, H_q, H_kv, S, kv, D, 91)
+    l1 = torch.tensor([k0], dtype=torch.int32, device="cuda") if masked else None
+    l2 = torch.tensor([k0, kv - 7], dtype=torch.int32, device="cuda") if masked else None
+    O1, M1, L1 = kf.attn_fwd(Q[:1].contiguous(), K[:1].contiguous(), V[:1].contiguous(), return_stats=True,
+                             causal=True, kv_lens=l1)
+    O2, M2, L2 = kf.attn_fwd(Q, K, V, return_stats=True, causal=True, kv_lens=l2)
+    torch.cuda.synchronize()
+    assert torch.equal(O1[0], O2[0]), f"O differs: max {(O1[0] - O2[0]).abs().max().item():.3g}"
+    assert torch.equal(M1[0], M2[0]) and torch.equal(L1[0], L2[0]), "Mi / Li differ"
+    if masked:
+        empty = S - k0  # rows before this one see no key of batch 0
+        assert torch.count_nonzero(O2[0, :, :empty]).item() == 0
+        assert torch.isinf(M2[0, :, :empty]).all() and torch.count_nonzero(L2[0, :, :empty]).item() == 0
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_wide_causal_kernel_matches_oracle(D):
+    """Batch 1 of a B = 2 causal call (the wide causal kernel), heads 0 and
+    the last, against the fp64 oracle on the same fp16 inputs."""
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    S, kv, H_q, H_kv = 4096, 4608, 32, 8
+    name = kf.kernel_names(2, S, kv, H_q, H_kv, D, causal=True)
+    print("case D", D, name, flush=True)
+    assert name == f"kf_attn_prefill_wide_kernel<{D}, true, 1, true>", name
+    (q16, k16, v16), (Q, K, V) = _inputs(2, H_q, H_kv, S, kv, D, 123 + D)
+    O, Mi, Li = kf.attn_fwd(Q, K, V, return_stats=True, causal=True)
+    torch.cuda.synchronize()
+    O, Mi, Li = O.cpu().numpy(), Mi.cpu().numpy(), Li.cpu().numpy()
+    for h in (0, H_q - 1):
+        hk = h // (H_q // H_kv)
+        Or, Mr, Lr = orc.sdpa(q16[1:2, h:h + 1], k16[1:2, hk:hk + 1], v16[1:2, hk:hk + 1], causal=True)
+        ok, max_abs, rel = orc.within_tolerance(O[1:2, h:h + 1], Or)
+        assert ok, f"head {h}: max_abs={max_abs:.3g} rel={rel:.3g}"
+        assert np.abs(Mi[1, h] - Mr[0, 0]).max() <= 1e-4, "Mi"
+        assert (np.abs(Li[1, h] - Lr[0, 0]) / np.abs(Lr[0, 0])).max() <= 1e-3, "Li"

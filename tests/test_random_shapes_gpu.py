@@ -95,8 +95,8 @@ def _layout(kf, B, H_q, H_kv, q_len, kv_len, D, causal=False, masked=False):
     """(path, kernel) for decode, kernel "short32" / "short64" (one wave per
     split of that many keys) or "stream"; ("prefill", waves, kv_groups) for
     prefill, read from the kernel name (kf_attn_prefill_kernel<D, mask,
-    waves, kv_groups>), or ("prefill", "wide", kv_groups) for kf_attn_prefill_wide_kernel
-    with either mask flag."""
+    waves, kv_groups>), or ("prefill", "wide", kv_groups) for
+    kf_attn_prefill_wide_kernel<D, mask, kv_groups, causal two-block layout>."""
     p = kf.plan(B, q_len, kv_len, H_q, H_kv, D)
     if p.path not in ("prefill", "prefill_split"):
         return (p.path, f"short{p.kv_per_split}" if p.splits_per_block == 4 else "stream")
@@ -107,8 +107,8 @@ def _layout(kf, B, H_q, H_kv, q_len, kv_len, D, causal=False, masked=False):
             return ("prefill_split", "parts")
         waves, groups = (int(x) for x in name.rstrip(">").split(",")[-2:])
         return ("prefill_split", waves, groups)
-    if name.startswith("kf_attn_prefill_wide"):  # the wide kernel, masked or not
-        return ("prefill", "wide", int(name.rstrip(">").split(",")[-1]))
+    if name.startswith("kf_attn_prefill_wide"):  # <D, mask, kv_groups, causal two-block layout>
+        return ("prefill", "wide", int(name.rstrip(">").split(",")[2]))
     waves, groups = (int(x) for x in name.rstrip(">").split(",")[-2:])
     return ("prefill", waves, groups)
 

@@ -59,7 +59,7 @@ def test_trace_report_cuts_the_bench_into_its_shapes(tmp_path):
 def test_counter_report_derives_the_figures(tmp_path):
     """Five warmup dispatches (wild values) are skipped; the medians of the
     timed ones give the derived figures."""
-    name = "void kf::kf_attn_prefill_wide_kernel<128, false, 1>(kf::AttnParams)"
+    name = "void kf::kf_attn_prefill_wide_kernel<128, false, 1, false>(kf::AttnParams)"
 
     def pmc(target, label, values, trace=False):
         rows, tr = [], []
