@@ -308,3 +308,55 @@ def test_wide_causal_kernel_matches_oracle(D):
         assert ok, f"head {h}: max_abs={max_abs:.3g} rel={rel:.3g}"
         assert np.abs(Mi[1, h] - Mr[0, 0]).max() <= 1e-4, "Mi"
         assert (np.abs(Li[1, h] - Lr[0, 0]) / np.abs(Lr[0, 0])).max() <= 1e-3, "Li"
+
+
+def _causal_random_cases(n=12, seed=20261202):
+    """Seeded shapes that the planner sends to the causal two-block kernel
+    for the whole batch and to the 32-row kernel (one KV group) for each
+    sequence alone: GQA ratios 1-8, 1-8 KV heads, D = 64 / 128, q_len a
+    multiple of 64 from 1024 to 8192, keys from q_len / 2 + 2048 on, key
+    counts in some."""
+    import kernelfoundry_amd as kf
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        D = int(rng.choice([64, 128]))
+        H_kv = int(rng.choice([1, 2, 4, 8]))
+        H_q = H_kv * int(rng.choice([1, 2, 4, 8]))
+        B = int(rng.integers(2, 9))
+        q = 64 * int(rng.integers(16, 129))
+        kv = int(rng.integers(q // 2 + 2048, q + 3000))
+        lens = bool(rng.random() < 0.4)
+        if kf.kernel_names(B, q, kv, H_q, H_kv, D, causal=True, masked=lens) != \
+                f"kf_attn_prefill_wide_kernel<{D}, true, 1, true>":
+            continue
+        if kf.kernel_names(1, q, kv, H_q, H_kv, D, causal=True, masked=lens) != \
+                f"kf_attn_prefill_kernel<{D}, true, 8, 1>":
+            continue
+        if B * H_q * q * D * 2 > 1e9:
+            continue
+        kl = [int(x) for x in rng.integers(0, kv + 1, size=B)] if lens else None
+        out.append((B, H_q, H_kv, q, kv, D, kl, int(rng.integers(1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("case", _causal_random_cases(), ids=lambda c: "B{}_Hq{}_Hkv{}_q{}_kv{}_D{}_{}".format(
+    *c[:6], "lens" if c[6] is not None else "full"))
+def test_wide_causal_random_shapes_equal_256_row_kernel_bitwise(case):
+    import kernelfoundry_amd as kf
+    torch = _torch()
+    B, H_q, H_kv, q, kv, D, kl, seed = case
+    print("case", case[:7], flush=True)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Q = torch.randn(B, H_q, q, D, generator=g, device="cuda").half()
+    K = torch.randn(B, H_kv, kv, D, generator=g, device="cuda").half()
+    V = torch.randn(B, H_kv, kv, D, generator=g, device="cuda").half()
+    lens = None if kl is None else torch.tensor(kl, dtype=torch.int32, device="cuda")
+    O, M, L = kf.attn_fwd(Q, K, V, return_stats=True, causal=True, kv_lens=lens)
+    for b in range(B):
+        O1, M1, L1 = kf.attn_fwd(Q[b:b + 1].contiguous(), K[b:b + 1].contiguous(), V[b:b + 1].contiguous(),
+                                 return_stats=True, causal=True,
+                                 kv_lens=None if lens is None else lens[b:b + 1].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(O[b], O1[0]), f"batch {b}: O differs by {(O[b] - O1[0]).abs().max().item():.3g}"
+        assert torch.equal(M[b], M1[0]) and torch.equal(L[b], L1[0]), f"batch {b}: Mi / Li differ"
